@@ -1,0 +1,377 @@
+"""Benchmark of the xinfer attention hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu-baseline]
+
+A step is one pass of the hot path over one batch: the in-place KV append of
+each row's new tokens followed by one attention call over the populated
+prefixes (torch.ops.xinfer.append_kv_batched + batched_flash_attention /
+flash_attention, the adapters' order).  Inputs are seeded synthetic bf16
+tensors resident in HBM before timing starts.
+
+The headline workload is BASELINE.json configs[1] (512-token chunked prefill
+at offset 1536, Qwen3-0.6B shapes): ``value`` is its whole-step TFLOP/s.  The
+same line carries the ragged batch-8 decode (configs[2], seed 0) as
+``decode`` with its KV GB/s, and with ``--all`` every configuration.
+
+Timing: each workload keeps several copies of its caches and rotates through
+them so consecutive steps never find their KV in the 256 MB Infinity Cache.
+One step per copy is captured in a HIP graph (the serving loop's launch
+path); the timed region replays exactly K steps between two device
+synchronisations.  The roofline figure of the dominant kernel is measured
+separately with HIP events on the launch stream around graph replays of the
+attention operator alone, and divides the algorithmic work (KV bytes for
+decode, causal FLOPs for prefill) by that average duration.
+
+The CPU baseline times the numpy oracle (fp32) on the host cores over a
+bounded sample of the same workload, and, as BASELINE.md plans, torch's CPU
+SDPA on bf16 tensors (the reference CPU path), both with thread counts.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+from pathlib import Path
+import sys
+import time
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2516.6
+MALL_BYTES = 256 << 20
+METRIC = "decode attn KV GB/s (% HBM peak) + prefill TFLOP/s (% MFMA), bs 1–8 ragged"
+
+
+def log(message):
+    print(message, file=sys.stderr, flush=True)
+
+
+class Runner:
+    """Device state of one workload: rotating cache copies and captured step graphs."""
+
+    def __init__(self, w, inputs, use_graphs=True):
+        import torch
+
+        from xinfer_amd.attention import batched_attention_metadata, cache_extent
+
+        self.w, self.torch = w, torch
+        device = "cuda"
+        populated = w.kv_bytes()
+        self.copies = max(2, min(8, -(-2 * MALL_BYTES // max(populated, 1)) + 1))
+        self.q = inputs["q"].to(device)
+        self.new_k = inputs["new_k"].to(device)
+        self.new_v = inputs["new_v"].to(device)
+        self.positions = inputs["positions"].to(device)
+        self.caches = []
+        for _ in range(self.copies):
+            self.caches.append((inputs["k"].to(device), inputs["v"].to(device)))
+        counts = torch.tensor(w.counts, dtype=torch.int32)
+        lengths = torch.tensor(w.lengths, dtype=torch.int32)
+        self.host, self.cu, self.blocks = batched_attention_metadata(lengths, counts, device)
+        self.extent = cache_extent(w.lengths[0])
+        self.outputs = {}
+        self.use_graphs = use_graphs
+        self.step_graphs = self.cycle_graph = self.attention_graph = None
+        self.cycle = self.copies
+
+    def attention(self, i):
+        ops = self.torch.ops.xinfer
+        k, v = self.caches[i % self.copies]
+        if self.w.op == "flash":
+            return ops.flash_attention(self.q, k, v, self.extent, self.w.scale)
+        return ops.batched_flash_attention(self.q, k, v, self.host, self.cu, self.blocks, self.w.scale)
+
+    def step(self, i):
+        k, v = self.caches[i % self.copies]
+        if self.w.append:
+            self.torch.ops.xinfer.append_kv_batched(self.new_k, self.new_v, self.positions, self.cu[0], k, v)
+        self.outputs[i] = self.attention(i)
+
+    def capture(self):
+        """Graphs: one step per cache copy, a cycle of S steps, and S attention-only calls.
+
+        S is a multiple of the copy count covering at least 16 steps, so one replay
+        amortises the host's launch cost over many device steps.
+        """
+        torch = self.torch
+        if not self.use_graphs:
+            return False
+        self.cycle = self.copies * max(1, -(-16 // self.copies))
+        try:
+            for i in range(self.copies):
+                self.step(i)
+            torch.cuda.synchronize()
+            eager = [self.outputs[i].clone() for i in range(self.copies)]
+            self.step_graphs = []
+            for i in range(self.copies):
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    self.step(i)
+                self.step_graphs.append((graph, self.outputs[i]))
+            self.cycle_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.cycle_graph):
+                for i in range(self.cycle):
+                    self.step(i)
+            cycle_outputs = [self.outputs[i] for i in range(self.copies)]
+            self.attention_graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(self.attention_graph):
+                self.attention_outputs = [self.attention(i) for i in range(self.cycle)]
+            # Replays must reproduce the eager results bit for bit.
+            for _ in range(2):
+                for graph, _ in self.step_graphs:
+                    graph.replay()
+                self.cycle_graph.replay()
+                self.attention_graph.replay()
+                torch.cuda.synchronize()
+                for i in range(self.cycle):
+                    reference = eager[i % self.copies]
+                    if not torch.equal(self.attention_outputs[i], reference):
+                        raise RuntimeError("attention graph replay differs from eager execution")
+                for i, (_, out) in enumerate(self.step_graphs):
+                    if not (torch.equal(out, eager[i]) and torch.equal(cycle_outputs[i], eager[i])):
+                        raise RuntimeError("step graph replay differs from eager execution")
+            return True
+        except Exception as error:  # capture unsupported: fall back to eager launches
+            log(f"graph capture unavailable ({error}); timing eager launches")
+            self.step_graphs = self.cycle_graph = self.attention_graph = None
+            self.use_graphs = False
+            return False
+
+    def run_steps(self, count):
+        if self.step_graphs is None:
+            for i in range(count):
+                self.step(i)
+            return
+        for _ in range(count // self.cycle):
+            self.cycle_graph.replay()
+        for i in range(count % self.cycle):
+            self.step_graphs[i % self.copies][0].replay()
+
+    def timed_steps(self, steps):
+        torch = self.torch
+        torch.cuda.synchronize()
+        start = time.perf_counter()
+        self.run_steps(steps)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - start) / steps
+
+    def attention_duration(self, launches):
+        """Average device time of one attention op: HIP events on the launch stream."""
+        torch = self.torch
+        stream = torch.cuda.current_stream()
+        per_round = self.cycle if self.attention_graph is not None else self.copies
+        rounds = max(1, launches // per_round)
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        start.record(stream)
+        for _ in range(rounds):
+            if self.attention_graph is not None:
+                self.attention_graph.replay()
+            else:
+                for i in range(self.copies):
+                    self.attention(i)
+        end.record(stream)
+        end.synchronize()
+        return start.elapsed_time(end) / 1e3 / (rounds * per_round)
+
+
+def cpu_baseline(w, inputs, budget_s):
+    """Oracle (fp32 numpy) and torch CPU SDPA (bf16) on a bounded sample of the workload."""
+    import numpy as np
+    import torch
+    import torch.nn.functional as F
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+
+    from oracle import attention as oracle
+
+    rows = list(range(w.batch))
+    counts = [w.counts[r] for r in rows]
+    lengths = [w.lengths[r] for r in rows]
+    # The sample: the rows' populated prefixes, widened once (resident inputs).
+    q = [inputs["q"][r : r + 1, :, : counts[i]].float().numpy() for i, r in enumerate(rows)]
+    k = [inputs["k_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
+    v = [inputs["v_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
+
+    def oracle_step():
+        for i in range(len(rows)):
+            oracle.attention(q[i], k[i], v[i], [counts[i]], [lengths[i]], w.scale, dtype=np.float32)
+
+    qb = [inputs["q"][r : r + 1, :, : counts[i]] for i, r in enumerate(rows)]
+    kb = [inputs["k_after"][r : r + 1, :, : lengths[i]] for i, r in enumerate(rows)]
+    vb = [inputs["v_after"][r : r + 1, :, : lengths[i]] for i, r in enumerate(rows)]
+    masks = [torch.arange(L)[None, :] <= torch.arange(L - n, L)[:, None] for n, L in zip(counts, lengths)]
+
+    def sdpa_step():
+        with sdpa_kernel(SDPBackend.MATH):
+            for i in range(len(rows)):
+                F.scaled_dot_product_attention(qb[i], kb[i], vb[i], attn_mask=masks[i], enable_gqa=True,
+                                               scale=w.scale)
+
+    def timeit(function):
+        function()  # warm-up
+        times = []
+        deadline = time.perf_counter() + budget_s
+        while len(times) < 3 or (time.perf_counter() < deadline and len(times) < 50):
+            start = time.perf_counter()
+            function()
+            times.append(time.perf_counter() - start)
+        times.sort()
+        return times[len(times) // 2], len(times)
+
+    oracle_s, oracle_reps = timeit(oracle_step)
+    sdpa_s, sdpa_reps = timeit(sdpa_step)
+    try:
+        from threadpoolctl import threadpool_info
+
+        blas_threads = max((info.get("num_threads", 1) for info in threadpool_info()), default=1)
+    except Exception:
+        blas_threads = os.cpu_count()
+    cpu_model = ""
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                cpu_model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return dict(oracle_s=oracle_s, oracle_reps=oracle_reps, sdpa_s=sdpa_s, sdpa_reps=sdpa_reps,
+                blas_threads=blas_threads, torch_threads=torch.get_num_threads(), cpu_model=cpu_model,
+                os_cpus=os.cpu_count())
+
+
+def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
+    import torch
+
+    from xinfer_amd import workloads
+
+    w = workloads.config(index, seed)
+    log(f"[bench] {w.name}: B={w.batch} Hq={w.heads} Hkv={w.kv_heads} D={w.dim} C={w.capacity} "
+        f"new={w.counts} L={w.lengths}")
+    inputs = workloads.make_inputs(w)
+    runner = Runner(w, inputs, use_graphs)
+    with torch.inference_mode():
+        graphs = runner.capture()
+        runner.run_steps(warmup)
+        seconds = runner.timed_steps(steps)
+        op_seconds = runner.attention_duration(max(steps, 4 * runner.copies))
+    decode = w.kind == "decode"
+    work = w.kv_bytes() if decode else w.flops()
+    scale = 1e9 if decode else 1e12
+    unit = "GB/s" if decode else "TFLOP/s"
+    peak = HBM_PEAK_GBS if decode else BF16_PEAK_TFLOPS
+    achieved = work / op_seconds / scale
+    result = {
+        "workload": w.name,
+        "value": work / seconds / scale,
+        "unit": unit,
+        "ms_per_step": seconds * 1e3,
+        "attention_op_us": op_seconds * 1e6,
+        "graph_replay": graphs,
+        "cache_copies": runner.copies,
+        "roofline": {
+            "bound": "hbm" if decode else "mfma",
+            "kernel": "decode_kernel + finalize_kernel" if decode else "prefill_kernel + finalize_kernel",
+            "achieved": achieved,
+            "peak": peak,
+            "unit": unit,
+            "frac": achieved / peak,
+            "traffic": None,
+            "algorithmic_per_launch": work,
+        },
+        "config": w.summary(),
+    }
+    log(f"[bench] {w.name}: {result['value']:.1f} {unit} per step ({seconds * 1e6:.1f} us), "
+        f"attention op {op_seconds * 1e6:.1f} us = {achieved:.1f} {unit} ({100 * achieved / peak:.1f}% of peak)")
+    if with_cpu:
+        cpu = cpu_baseline(w, inputs, cpu_budget)
+        result["cpu_baseline"] = {
+            "value": work / cpu["oracle_s"] / scale,
+            "unit": unit,
+            "cores": cpu["blas_threads"],
+            "kind": "port",
+            "sample": f"one full step of {w.name} (all {w.batch} rows, fp32 numpy oracle), "
+                      f"median of {cpu['oracle_reps']} runs",
+            "reference_cpu_sdpa": {
+                "value": work / cpu["sdpa_s"] / scale,
+                "unit": unit,
+                "threads": cpu["torch_threads"],
+                "dtype": "bf16",
+                "median_ms": cpu["sdpa_s"] * 1e3,
+                "runs": cpu["sdpa_reps"],
+            },
+            "cpu_model": cpu["cpu_model"],
+            "os_cpu_count": cpu["os_cpus"],
+        }
+        log(f"[bench] {w.name}: CPU oracle {result['cpu_baseline']['value']:.3g} {unit} "
+            f"({cpu['blas_threads']} threads); CPU SDPA bf16 {work / cpu['sdpa_s'] / scale:.3g} {unit} "
+            f"({cpu['torch_threads']} threads)")
+    del runner
+    torch.cuda.empty_cache()
+    return result
+
+
+def main():
+    parser = argparse.ArgumentParser(description="xinfer attention hot-path benchmark (one MI355X)")
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=200)
+    parser.add_argument("--warmup", type=int, default=20)
+    parser.add_argument("--all", action="store_true", help="also measure configs 1, 4, 5 and cfg3 seeds 0-7")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
+    parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
+              "The attention operator would shard by rows or KV heads with no exchange; see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    from xinfer_amd.attention import load_attention_ops
+    from xinfer_amd.build import library_path
+
+    load_attention_ops(library_path())
+    with_cpu = not args.no_cpu_baseline
+    prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
+    decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
+    extra = []
+    if args.all:
+        for index, seed in [(1, 0), (4, 0), (5, 0)] + [(3, s) for s in range(1, 8)]:
+            extra.append(measure(index, seed, args.steps, args.warmup, not args.eager, False, args.cpu_budget))
+    line = {
+        "metric": METRIC,
+        "value": prefill["value"],
+        "unit": prefill["unit"],
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": prefill["ms_per_step"],
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) bf16 Q/K/V; no checkpoints)",
+        "config": {
+            **prefill["config"],
+            "global_batch": prefill["config"]["batch"],
+            "seq_len": 2048,
+            "parallelism": "single GPU",
+            "graph_replay": prefill["graph_replay"],
+        },
+        "roofline": prefill["roofline"],
+        "cpu_baseline": prefill.get("cpu_baseline"),
+        "decode": decode,
+    }
+    if extra:
+        line["configs"] = extra
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,112 @@
+/*
+ * C ABI of libxinfer_attention_ops.so: attention over each request's populated
+ * KV prefix and the in-place KV-cache append, for AMD MI355X (gfx950).
+ *
+ * Every entry point takes plain device pointers, element strides and host-side
+ * lengths; none allocates device memory and none synchronises the host with the
+ * device.  Work is enqueued on `stream` (a hipStream_t; NULL is the null stream).
+ * Tensors are bf16 (stored as raw uint16 bits).  Return value: 0 on success, or
+ * a status code whose message `xinfer_status_string` returns.  The messages
+ * reproduce the reference operator's TORCH_CHECK texts where one exists.
+ *
+ * The torch.library operators and the AOTInductor C shims that the reference
+ * exports are defined in the same library; they validate torch-specific
+ * properties and call the entry points below.
+ */
+#ifndef XINFER_ATTENTION_H
+#define XINFER_ATTENTION_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Messages (xinfer_status_string) follow the reference:
+ * compiler/common/kernels/attention.cpp:17-35 and :84-104. */
+enum {
+  XINFER_OK = 0,
+  XINFER_ERR_QKV_SHAPES = 1,      /* "Invalid Q/K/V shapes"                        attention.cpp:17-19 */
+  XINFER_ERR_Q_SHAPE = 2,         /* "Unsupported Q shape"                         attention.cpp:90-91 */
+  XINFER_ERR_KV_SHAPE = 3,        /* "Expected matching full-capacity K/V ..."     attention.cpp:92-94 */
+  XINFER_ERR_HEADS = 4,           /* "Query heads must be a positive multiple ..." attention.cpp:95-96 */
+  XINFER_ERR_HEAD_DIM = 5,        /* "Flash head dimension must be ..."            attention.cpp:97-98 */
+  XINFER_ERR_PREFIX = 6,          /* "Invalid valid-prefix length"                 attention.cpp:102 */
+  XINFER_ERR_SCALE = 7,           /* "Attention scale must be finite and positive" attention.cpp:103 */
+  XINFER_ERR_OFFSETS_START = 8,   /* "Cumulative lengths must start at zero"       attention.cpp:35 */
+  XINFER_ERR_LENGTHS = 9,         /* "Invalid query/KV lengths"                    attention.cpp:43-45 */
+  XINFER_ERR_WORKSPACE = 10,      /* workspace smaller than the *_workspace_size query */
+  XINFER_ERR_LAYOUT = 11,         /* feature stride != 1 or rows not 16-byte aligned */
+  XINFER_ERR_CACHE = 12,          /* cache tensors not contiguous [B,H,C,D] / shape mismatch */
+  XINFER_ERR_LAUNCH = 13,         /* a HIP kernel launch failed */
+  XINFER_ERR_ARGUMENT = 14        /* null pointer or negative size */
+};
+
+/* A strided rank-4 view of bf16 device memory, [batch, heads, sequence, dim].
+ * Strides are in elements.  The attention kernels need stride[3] == 1, the
+ * other strides multiples of 8 and `data` 16-byte aligned (XINFER_ERR_LAYOUT
+ * otherwise); the append kernel accepts any strides for key/value. */
+typedef struct xinfer_view4 {
+  const void *data;
+  int64_t size[4];
+  int64_t stride[4];
+} xinfer_view4;
+
+/* Message for a status code (static storage, never NULL). */
+const char *xinfer_status_string(int status);
+
+/* ---------------------------------------------------------------------------
+ * xinfer::flash_attention -- replaces compiler/common/kernels/attention.cpp:82-124
+ * (schema :133-134, fake compiler/common/attention.py:63-83).
+ *
+ * q [B,Hq,T,D], k/v [B,Hkv,C,D]; every row attends with all T queries over the
+ * first `valid_length` cache positions, lower-right causal: query i sees keys
+ * j <= valid_length - T + i.  out: contiguous [B,Hq,T,D] bf16, written fully.
+ * ------------------------------------------------------------------------- */
+size_t xinfer_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
+                                             int64_t valid_length);
+int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                           int64_t valid_length, double scale, void *out, void *workspace,
+                           size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * xinfer::batched_flash_attention -- replaces attention.cpp:14-79
+ * (schema :129-131, fake compiler/common/attention.py:86-94).
+ *
+ * host_offsets: host int32 [2][B+1]; row 0 = cumulative real-query counts,
+ * row 1 = cumulative populated KV lengths (both start at 0), exactly the CPU
+ * `offsets` tensor of batched_attention_metadata (attention.py:27-40).  Row r
+ * attends with its first count_r queries over k/v[r, :, :L_r], lower-right
+ * causal; out[r, :, count_r:] is written as zeros.
+ * ------------------------------------------------------------------------- */
+size_t xinfer_batched_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
+                                                     const int32_t *host_offsets);
+int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
+                                   const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                   void *out, void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * xinfer::append_kv_batched -- replaces the Triton op
+ * compiler/common/kernels/kv_cache.py:8-72.
+ *
+ * cache_key[r,h,positions[r,t],:] = key[r,h,t,:] (same for value) for
+ * t < count_r = cu_query[r+1] - cu_query[r]; positions of padded tokens are
+ * never read.  positions: device int64 [B,T] with strides (pos_stride_b,
+ * pos_stride_t); cu_query: device int32 [B+1].  Caches are contiguous
+ * [B,Hkv,C,D] bf16 and are the only memory written.  A position outside
+ * [0, C) is skipped instead of being written out of bounds.
+ * ------------------------------------------------------------------------- */
+int xinfer_append_kv_batched(const xinfer_view4 *key, const xinfer_view4 *value,
+                             const int64_t *positions, int64_t pos_stride_b, int64_t pos_stride_t,
+                             const int32_t *cu_query, const xinfer_view4 *cache_key,
+                             const xinfer_view4 *cache_value, void *stream);
+
+/* The AOTInductor C shims of the same library are declared in
+ * xinfer_attention_aoti.h. */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XINFER_ATTENTION_H */

@@ -1,0 +1,54 @@
+/*
+ * AOTInductor C shims exported by libxinfer_attention_ops.so.
+ *
+ * These are the symbols a generated AOTI wrapper.cpp calls directly when
+ * torch._inductor.config.aot_inductor.custom_ops_to_c_shims maps the xinfer
+ * operators to them (compiler/common/package.py:55-78).  Input handles are
+ * borrowed; the output handle is a new tensor whose ownership passes to the
+ * caller.  Errors (the operators' TORCH_CHECK messages) are reported as
+ * AOTI_TORCH_FAILURE with the message stored by torch's error bridge.
+ *
+ * The handle types are the opaque ones of torch/csrc/inductor/aoti_torch/c/shim.h.
+ */
+#ifndef XINFER_ATTENTION_AOTI_H
+#define XINFER_ATTENTION_AOTI_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+struct AtenTensorOpaque;
+typedef AtenTensorOpaque *AtenTensorHandle;
+#else
+typedef struct AtenTensorOpaque *AtenTensorHandle;
+#endif
+typedef int32_t AOTITorchError;
+
+/* Replaces compiler/common/kernels/attention_shim.cpp:21-32 (declared as a
+ * string at compiler/common/attention.py:10-12). */
+AOTITorchError aoti_torch_cuda_flash_attention(AtenTensorHandle q, AtenTensorHandle k,
+                                               AtenTensorHandle v, AtenTensorHandle extent,
+                                               double scale, AtenTensorHandle *output);
+
+/* Replaces compiler/common/kernels/attention_shim.cpp:5-19 (declared as a
+ * string at compiler/common/attention.py:13-16). */
+AOTITorchError aoti_torch_cuda_batched_flash_attention(AtenTensorHandle q, AtenTensorHandle k,
+                                                       AtenTensorHandle v, AtenTensorHandle offsets,
+                                                       AtenTensorHandle cuda_offsets,
+                                                       AtenTensorHandle blocks, double scale,
+                                                       AtenTensorHandle *output);
+
+/* New: the reference's append is a Triton op (compiler/common/kernels/kv_cache.py:45-72)
+ * that AOTI compiles into the wrapper; the native op needs its own shim.  It
+ * mutates cache_key/cache_value in place and returns no handle. */
+AOTITorchError aoti_torch_cuda_append_kv_batched(AtenTensorHandle key, AtenTensorHandle value,
+                                                 AtenTensorHandle positions,
+                                                 AtenTensorHandle cu_query,
+                                                 AtenTensorHandle cache_key,
+                                                 AtenTensorHandle cache_value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* XINFER_ATTENTION_AOTI_H */

@@ -1,0 +1,246 @@
+"""GPU checks of the xinfer attention operators, mirroring the reference's op tests.
+
+Counterpart of compiler/common/tests/test_attention.py:19-346 and
+compiler/qwen35/tests/test_attention.py:244-297.  The reference's bitwise
+comparisons against ATen's own flash kernel pin ATen's rounding rather than the
+operator contract; they are replaced by the fp32 reference bounds the reference
+uses everywhere else (relative L2 < 0.01, peak relative <= 0.05) plus the
+BASELINE gates (max-abs <= 2e-2, mean-abs <= 2e-3).  Determinism, isolation
+from other rows and from unused cache slots, zeroed padding, read-only inputs
+and the fake contract are checked bit for bit as in the reference.
+"""
+
+import pytest
+import torch
+
+from attn_helpers import assert_close_rows, log, reference_attention
+from xinfer_amd.attention import batched_attention_metadata, cache_extent
+from xinfer_amd.kv_cache import append_kv_batched
+
+pytestmark = pytest.mark.gpu
+
+
+def inputs(heads, kv_heads, dim, tokens, feature_stride=1, capacity=1024, batch_size=1):
+    options = dict(device="cuda", dtype=torch.bfloat16)
+    q = torch.randn(batch_size, heads, tokens, dim * feature_stride, **options)[..., ::feature_stride]
+    k = torch.randn(batch_size, kv_heads, capacity, dim * feature_stride, **options)[..., ::feature_stride]
+    v = torch.randn(batch_size, kv_heads, capacity, dim * feature_stride, **options)[..., ::feature_stride]
+    return q, k, v
+
+
+@torch.inference_mode()
+def test_batched_attention_and_masked_writes(gpu_ops):
+    torch.manual_seed(18)
+    op = gpu_ops.batched_flash_attention.default
+    for batch in range(1, 9):
+        for width, start, capacity, ragged in (
+            (1, 17, 1024, False),
+            (1, 17, 1024, True),
+            (2, 511, 513, True),
+            (17, 7, 1024, True),
+            (512, 1, 1024, True),
+            (512, 2048, 4096, True),
+        ):
+            counts = [width if not ragged or r % 3 == 0 else (0 if r % 3 == 1 else 1) for r in range(batch)]
+            starts = [start - r if start >= batch else start for r in range(batch)]
+            lengths = [s + c for s, c in zip(starts, counts)]
+            log(f"batched batch={batch} width={width} counts={counts} lengths={lengths} capacity={capacity}")
+            q, k, v = inputs(16, 8, 128, width, capacity=capacity, batch_size=batch)
+            key = torch.randn(batch, width, 8, 128, device="cuda", dtype=q.dtype).transpose(1, 2)
+            value = torch.randn_like(key)
+            positions = torch.stack([torch.arange(s, s + width, device="cuda") for s in starts])
+            host, cu, blocks = batched_attention_metadata(
+                torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), q.device
+            )
+            if not ragged:
+                blocks = blocks.as_strided((batch, 1), (1, 0))
+            expected_k, expected_v = k.clone(), v.clone()
+            for row, (count, offset) in enumerate(zip(counts, starts)):
+                expected_k[row, :, offset : offset + count] = key[row, :, :count]
+                expected_v[row, :, offset : offset + count] = value[row, :, :count]
+                positions[row, count:] = capacity + 100  # padded positions are never dereferenced
+            before_inputs = [t.clone() for t in (key, value, positions)]
+            append_kv_batched(key, value, positions, cu[0], k, v)
+            assert torch.equal(k, expected_k) and torch.equal(v, expected_v)
+            assert all(torch.equal(a, b) for a, b in zip((key, value, positions), before_inputs))
+            actual = op(q, k, v, host, cu, blocks, 128**-0.5)
+            assert actual.stride() == torch.empty(q.shape).stride()
+            assert actual.data_ptr() not in [t.data_ptr() for t in (q, k, v)]
+            expected = reference_attention(q, k, v, counts, lengths, 128**-0.5)
+            for row, count in enumerate(counts):
+                assert torch.count_nonzero(actual[row, :, count:]).item() == 0
+            assert_close_rows(actual, expected, counts)
+            for row, (count, length) in enumerate(zip(counts, lengths)):
+                q[row, :, count:] = float("nan")
+                k[row, :, length:] = float("nan")
+                v[row, :, length:] = float("nan")
+            assert torch.equal(actual, op(q, k, v, host, cu, blocks, 128**-0.5))
+            if batch > 1:
+                k[0].fill_(5)
+                v[0].fill_(7)
+                assert torch.equal(actual[1:], op(q, k, v, host, cu, blocks, 128**-0.5)[1:])
+            torch.library.opcheck(op, (q, k, v, host, cu, blocks, 128**-0.5),
+                                  test_utils=("test_schema", "test_faketensor"))
+
+
+@torch.inference_mode()
+def test_appended_prefill_batches(gpu_ops):
+    torch.manual_seed(18)
+    op = gpu_ops.flash_attention.default
+    for batch_size in (1, 2):
+        for length in (1024, 2560):
+            log(f"appended prefill batch={batch_size} length={length}")
+            q, k, v = inputs(16, 8, 128, 512, capacity=4096, batch_size=batch_size)
+            extent = cache_extent(length)
+            actual = op(q, k, v, extent, 128**-0.5)
+            expected = reference_attention(q, k, v, [512] * batch_size, [length] * batch_size, 128**-0.5)
+            assert_close_rows(actual, expected, [512] * batch_size)
+            k[:, :, length:].fill_(100)
+            v[:, :, length:].fill_(-100)
+            assert torch.equal(actual, op(q, k, v, extent, 128**-0.5))
+            if batch_size == 2:
+                k[0].fill_(5)
+                v[0].fill_(7)
+                assert torch.equal(actual[1], op(q, k, v, extent, 128**-0.5)[1])
+
+
+@torch.inference_mode()
+def test_two_independent_rows(gpu_ops):
+    torch.manual_seed(13)
+    op = gpu_ops.flash_attention.default
+    for tokens, length in ((1, 32), (2, 3), (16, 32), (512, 512)):
+        log(f"two rows tokens={tokens} length={length}")
+        triples = [inputs(16, 8, 128, tokens) for _ in range(2)]
+        q, k, v = [torch.cat([triple[i] for triple in triples]) for i in range(3)]
+        extent = cache_extent(length)
+        out = op(q, k, v, extent, 128**-0.5)
+        separate = torch.cat([op(*triple, extent, 128**-0.5) for triple in triples])
+        # The schedule depends only on lengths, so rows computed alone are bit-identical.
+        assert torch.equal(out, separate)
+        expected = reference_attention(q, k, v, [tokens] * 2, [length] * 2, 128**-0.5)
+        assert_close_rows(out, expected, [tokens] * 2)
+        assert out.shape == q.shape
+        k[0].fill_(5)
+        v[0].fill_(7)
+        assert torch.equal(out[1], op(q, k, v, extent, 128**-0.5)[1])
+        torch.library.opcheck(op, (q, k, v, extent, 128**-0.5))
+
+
+@torch.inference_mode()
+def test_grouped_prefix_and_read_only_contract(gpu_ops):
+    torch.manual_seed(35)
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):
+        for tokens, length in ((1, 1), (1, 2), (1, 32), (1, 129), (1, 1024), (2, 2), (2, 3), (16, 32),
+                               (16, 129), (510, 1022), (512, 512), (512, 1024)):
+            log(f"grouped heads={heads}/{kv_heads} dim={dim} tokens={tokens} length={length}")
+            q, k, v = inputs(heads, kv_heads, dim, tokens)
+            before = [t.clone() for t in (q, k, v)]
+            extent = cache_extent(length)
+            actual = op(q, k, v, extent, dim**-0.5)
+            assert actual.stride() == (heads * tokens * dim, tokens * dim, dim, 1)
+            assert actual.data_ptr() not in [t.data_ptr() for t in (q, k, v)]
+            for tensor, original in zip((q, k, v), before):
+                assert torch.equal(tensor, original)
+            expected = reference_attention(q, k, v, [tokens], [length], dim**-0.5)
+            assert_close_rows(actual, expected, [tokens])
+            k[:, :, length:].fill_(100)
+            v[:, :, length:].fill_(-100)
+            extent.fill_(255)
+            assert torch.equal(actual, op(q, k, v, extent, dim**-0.5))
+            checks = torch.library.opcheck(op, (q, k, v, extent, dim**-0.5))
+            assert all(value == "SUCCESS" for value in checks.values())
+
+
+@torch.inference_mode()
+def test_long_prefix_and_tensor_derived_capacity(gpu_ops):
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim in ((16, 8, 128), (16, 4, 256)):
+        for length in (8192, 8193, 16384):
+            log(f"long prefix heads={heads}/{kv_heads} dim={dim} length={length}")
+            q, k, v = inputs(heads, kv_heads, dim, 2, capacity=16384)
+            extent = cache_extent(length)
+            actual = op(q, k, v, extent, dim**-0.5)
+            expected = reference_attention(q, k, v, [2], [length], dim**-0.5)
+            assert_close_rows(actual, expected, [2])
+            k[:, :, length:].fill_(100)
+            v[:, :, length:].fill_(-100)
+            assert torch.equal(actual, op(q, k, v, extent, dim**-0.5))
+            torch.library.opcheck(op, (q, k, v, extent, dim**-0.5), test_utils=("test_schema", "test_faketensor"))
+            with pytest.raises(RuntimeError, match="Invalid valid-prefix length"):
+                op(q, k, v, cache_extent(16385), dim**-0.5)
+
+
+@torch.inference_mode()
+def test_appended_chunks_use_lower_right_causality(gpu_ops):
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):
+        log(f"known answer heads={heads}/{kv_heads} dim={dim}")
+        q, k, v = inputs(heads, kv_heads, dim, 2)
+        q.zero_()
+        k.zero_()
+        v.copy_(torch.arange(1024, device="cuda", dtype=torch.bfloat16)[None, None, :, None])
+        output = op(q, k, v, cache_extent(5), dim**-0.5)
+        expected = torch.tensor([1.5, 2.0], device="cuda", dtype=torch.bfloat16)
+        assert torch.equal(output, expected[None, None, :, None].expand_as(output))
+
+
+@torch.inference_mode()
+def test_feature_strides_and_fake_contract(gpu_ops):
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):
+        log(f"feature stride 2 heads={heads}/{kv_heads} dim={dim}")
+        q, k, v = inputs(heads, kv_heads, dim, 2, feature_stride=2)
+        extent = cache_extent(3)
+        output = op(q, k, v, extent, dim**-0.5)
+        contiguous = op(q.contiguous(), k[:, :, :3].contiguous(), v[:, :, :3].contiguous(), extent, dim**-0.5)
+        assert torch.equal(output, contiguous)
+        checks = torch.library.opcheck(op, (q, k, v, extent, dim**-0.5))
+        assert all(value == "SUCCESS" for value in checks.values())
+
+
+@torch.inference_mode()
+def test_invalid_extent_and_head_dimensions(gpu_ops):
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):
+        q, k, v = inputs(heads, kv_heads, dim, 2)
+        for length in (0, 1, 1025):
+            with pytest.raises(RuntimeError, match="Invalid valid-prefix length"):
+                op(q, k, v, cache_extent(length), dim**-0.5)
+    q, k, v = inputs(8, 2, 256, 2)
+    log("invalid geometry")
+    assert op(q[:, :4], k, v, cache_extent(3), 256**-0.5).shape == q[:, :4].shape
+    with pytest.raises(RuntimeError, match="Query heads must be a positive multiple"):
+        op(q[:, :3], k, v, cache_extent(3), 256**-0.5)
+    for dim in (7, 127, 264):
+        invalid = inputs(8, 2, dim, 2)
+        with pytest.raises(RuntimeError, match="Flash head dimension"):
+            op(*invalid, cache_extent(3), dim**-0.5)
+    with pytest.raises(RuntimeError, match="Attention scale must be finite and positive"):
+        op(q, k, v, cache_extent(3), -1.0)
+
+
+@torch.inference_mode()
+def test_input_derived_gqa_geometry(gpu_ops):
+    """compiler/qwen35/tests/test_attention.py:244-297, against an explicit fp32 softmax."""
+    for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256), (16, 4, 256), (6, 2, 64)):
+        log(f"geometry heads={heads}/{kv_heads} dim={dim}")
+        q = torch.randn(1, heads, 16, dim, device="cuda", dtype=torch.bfloat16)
+        k, v = (torch.randn(1, kv_heads, 16384, dim, device="cuda", dtype=torch.bfloat16) for _ in range(2))
+        extent, scale = cache_extent(129), dim**-0.5
+        actual = gpu_ops.flash_attention(q, k, v, extent, scale)
+        expected = reference_attention(q, k, v, [16], [129], scale)
+        assert actual.shape == q.shape and actual.is_contiguous()
+        assert ((actual.float() - expected).norm() / expected.norm()).item() <= 0.01
+        torch.library.opcheck(gpu_ops.flash_attention.default, (q, k, v, extent, scale),
+                              test_utils=("test_schema", "test_faketensor"))
+    for heads, kv_heads in ((0, 2), (8, 0), (3, 2)):
+        q = torch.randn(1, heads, 16, 128, device="cuda", dtype=torch.bfloat16)
+        k = torch.randn(1, kv_heads, 1024, 128, device="cuda", dtype=torch.bfloat16)
+        with pytest.raises(RuntimeError, match="Query heads"):
+            gpu_ops.flash_attention(q, k, k, cache_extent(129), 0.1)
+    for dim in (0, 7, 127, 264):
+        q = torch.randn(1, 8, 16, dim, device="cuda", dtype=torch.bfloat16)
+        k = torch.randn(1, 2, 1024, dim, device="cuda", dtype=torch.bfloat16)
+        with pytest.raises(RuntimeError, match="Flash head dimension"):
+            gpu_ops.flash_attention(q, k, k, cache_extent(129), 1.0)

@@ -1,0 +1,113 @@
+"""The C ABI called directly through ctypes, as a non-torch host would bind it.
+
+Device memory comes from torch (plumbing only); every compute call goes through
+the extern "C" entry points of include/xinfer_attention.h and must agree bit for
+bit with the torch operators built on the same kernels, and with the oracle.
+"""
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from attn_helpers import MAX_ABS, MEAN_ABS, log
+from oracle import attention as oracle
+from xinfer_amd.attention import batched_attention_metadata
+
+pytestmark = pytest.mark.gpu
+
+
+class View4(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("size", ctypes.c_int64 * 4), ("stride", ctypes.c_int64 * 4)]
+
+
+def view(t):
+    return View4(t.data_ptr(), (ctypes.c_int64 * 4)(*t.shape), (ctypes.c_int64 * 4)(*t.stride()))
+
+
+@pytest.fixture(scope="module")
+def capi(gpu_ops, library_path):
+    lib = ctypes.CDLL(str(library_path))
+    lib.xinfer_status_string.restype = ctypes.c_char_p
+    lib.xinfer_batched_flash_attention_workspace_size.restype = ctypes.c_size_t
+    lib.xinfer_flash_attention_workspace_size.restype = ctypes.c_size_t
+    return lib
+
+
+def stream():
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+@torch.inference_mode()
+def test_batched_through_c_abi(capi, gpu_ops):
+    torch.manual_seed(77)
+    batch, heads, kv_heads, dim, capacity = 4, 16, 4, 256, 2048
+    counts, lengths = [1, 300, 0, 2], [1800, 700, 9, 40]
+    log(f"C ABI batched counts={counts} lengths={lengths}")
+    q = torch.randn(batch, max(counts), heads, dim, device="cuda", dtype=torch.bfloat16).transpose(1, 2)
+    k = torch.randn(batch, kv_heads, capacity, dim, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    host, cu, blocks = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
+    qv, kv, vv = view(q), view(k), view(v)
+    offsets = host.contiguous()
+    host_ptr = ctypes.cast(offsets.data_ptr(), ctypes.POINTER(ctypes.c_int32))
+    size = capi.xinfer_batched_flash_attention_workspace_size(ctypes.byref(qv), ctypes.byref(kv), host_ptr)
+    workspace = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
+    status = capi.xinfer_batched_flash_attention(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, ctypes.c_double(dim**-0.5),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size), stream())
+    assert status == 0, capi.xinfer_status_string(status)
+    if size:
+        too_small = capi.xinfer_batched_flash_attention(
+            ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, ctypes.c_double(dim**-0.5),
+            ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size - 1),
+            stream())
+        assert capi.xinfer_status_string(too_small).decode().startswith("Attention workspace")
+    via_torch = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)
+    assert torch.equal(out.view(torch.int16), via_torch.view(torch.int16))
+    expected = oracle.attention(*(x.float().cpu().numpy().astype(np.float64) for x in (q, k, v)),
+                                counts, lengths, dim**-0.5)
+    delta = np.abs(out.float().cpu().numpy() - expected)
+    assert delta.max() <= MAX_ABS
+    for r, count in enumerate(counts):
+        assert not out[r, :, count:].any()
+        if count:
+            assert delta[r, :, :count].mean() <= MEAN_ABS
+
+
+@torch.inference_mode()
+def test_flash_and_append_through_c_abi(capi, gpu_ops):
+    torch.manual_seed(78)
+    heads, kv_heads, dim, capacity, tokens, length = 16, 8, 128, 4096, 512, 2048
+    log("C ABI flash + append")
+    q = torch.randn(1, heads, tokens, dim, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(1, kv_heads, capacity, dim, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    new_k = torch.randn(1, tokens, kv_heads, dim, device="cuda", dtype=torch.bfloat16).transpose(1, 2)
+    new_v = torch.randn_like(new_k)
+    positions = torch.arange(length - tokens, length, device="cuda")[None]
+    cu = torch.tensor([0, tokens], dtype=torch.int32, device="cuda")
+    expected_k, expected_v = k.clone(), v.clone()
+    expected_k[:, :, length - tokens : length] = new_k
+    expected_v[:, :, length - tokens : length] = new_v
+    status = capi.xinfer_append_kv_batched(
+        ctypes.byref(view(new_k)), ctypes.byref(view(new_v)), ctypes.c_void_p(positions.data_ptr()),
+        ctypes.c_int64(positions.stride(0)), ctypes.c_int64(positions.stride(1)), ctypes.c_void_p(cu.data_ptr()),
+        ctypes.byref(view(k)), ctypes.byref(view(v)), stream())
+    assert status == 0, capi.xinfer_status_string(status)
+    assert torch.equal(k, expected_k) and torch.equal(v, expected_v)
+    qv, kv, vv = view(q), view(k), view(v)
+    size = capi.xinfer_flash_attention_workspace_size(ctypes.byref(qv), ctypes.byref(kv), ctypes.c_int64(length))
+    workspace = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    status = capi.xinfer_flash_attention(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), ctypes.c_int64(length), ctypes.c_double(dim**-0.5),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size), stream())
+    assert status == 0, capi.xinfer_status_string(status)
+    from xinfer_amd.attention import cache_extent
+
+    via_torch = gpu_ops.flash_attention(q, k, v, cache_extent(length), dim**-0.5)
+    assert torch.equal(out.view(torch.int16), via_torch.view(torch.int16))

@@ -1,0 +1,120 @@
+"""Parity of one hot-path step (KV append + attention) on the five measured configurations.
+
+Inputs are the seeded CPU draws of xinfer_amd.workloads (identical bits for the
+GPU and the CPU oracle).  Gates: the KV caches after the append
+are bit-identical to the oracle append; attention outputs are within max-abs
+2e-2 and mean-abs 2e-3 of the float64 oracle; and the error is no worse than
+the reference path's own bf16 error -- torch SDPA on bf16 tensors with the
+explicit lower-right mask (the adapted eager attention), measured on the same
+inputs -- within the slack stated in BF16_SLACK.
+"""
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from attn_helpers import MAX_ABS, MEAN_ABS, log
+from oracle import attention as oracle
+from xinfer_amd import workloads
+from xinfer_amd.attention import batched_attention_metadata, cache_extent
+
+pytestmark = pytest.mark.gpu
+
+# Our error may exceed the bf16 reference path's error by at most this factor
+# (both are dominated by the final bf16 rounding of the output).
+BF16_SLACK = 1.25
+
+
+def row_slices(inputs, r, length, count):
+    k = inputs["k_after"][r : r + 1, :, :length]
+    v = inputs["v_after"][r : r + 1, :, :length]
+    q = inputs["q"][r : r + 1, :, :count]
+    return q, k, v
+
+
+def bf16_reference(q, k, v, count, length, scale):
+    """torch SDPA on bf16 CPU tensors with the explicit lower-right mask (reference path)."""
+    mask = torch.arange(length)[None, :] <= torch.arange(length - count, length)[:, None]
+    with sdpa_kernel(SDPBackend.MATH):
+        return F.scaled_dot_product_attention(q, k, v, attn_mask=mask, enable_gqa=True, scale=scale)
+
+
+def run_step(gpu_ops, w, inputs):
+    device = "cuda"
+    q = inputs["q"].to(device)
+    k = inputs["k"].to(device)
+    v = inputs["v"].to(device)
+    counts = torch.tensor(w.counts, dtype=torch.int32)
+    lengths = torch.tensor(w.lengths, dtype=torch.int32)
+    host, cu, blocks = batched_attention_metadata(lengths, counts, device)
+    if w.append:
+        new_k = inputs["new_k"].to(device)
+        new_v = inputs["new_v"].to(device)
+        positions = inputs["positions"].to(device)
+        gpu_ops.append_kv_batched(new_k, new_v, positions, cu[0], k, v)
+    if w.op == "flash":
+        out = gpu_ops.flash_attention(q, k, v, cache_extent(w.lengths[0]), w.scale)
+    else:
+        out = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, w.scale)
+    torch.cuda.synchronize()
+    return out.cpu(), k, v
+
+
+CASES = [(1, 0), (2, 0), (3, 0), (3, 3), (4, 0), (5, 0)]
+
+
+@pytest.mark.parametrize("index,seed", CASES, ids=[f"cfg{i}_seed{s}" for i, s in CASES])
+@torch.inference_mode()
+def test_config_parity(gpu_ops, index, seed):
+    w = workloads.config(index, seed)
+    log(f"config {w.name}: B={w.batch} Hq={w.heads} Hkv={w.kv_heads} D={w.dim} C={w.capacity} "
+        f"counts={w.counts} lengths={w.lengths}")
+    inputs = workloads.make_inputs(w)
+    out, k_gpu, v_gpu = run_step(gpu_ops, w, inputs)
+    if w.append:
+        # Bit-exact cache after the append, including every untouched slot.
+        assert torch.equal(k_gpu.cpu().view(torch.int16), inputs["k_after"].view(torch.int16))
+        assert torch.equal(v_gpu.cpu().view(torch.int16), inputs["v_after"].view(torch.int16))
+    del k_gpu, v_gpu
+    worst = dict(max_abs=0.0, sum_abs=0.0, n=0, ref_max_abs=0.0, ref_sum_abs=0.0, ref_n=0)
+    reference_rows = range(w.batch) if index != 5 else range(0, w.batch, 4)
+    for r, (count, length) in enumerate(zip(w.counts, w.lengths)):
+        assert torch.count_nonzero(out[r, :, count:]).item() == 0
+        q, k, v = row_slices(inputs, r, length, count)
+        expected = oracle.attention(*(oracle.bf16_to_f32(x.view(torch.int16).numpy().view(np.uint16)).astype(np.float64)
+                                      for x in (q, k, v)), [count], [length], w.scale)
+        delta = np.abs(out[r : r + 1, :, :count].float().numpy().astype(np.float64) - expected)
+        worst["max_abs"] = max(worst["max_abs"], float(delta.max()))
+        worst["sum_abs"] += float(delta.sum())
+        worst["n"] += delta.size
+        if r in reference_rows:
+            ref = bf16_reference(q, k, v, count, length, w.scale).float().numpy().astype(np.float64)
+            ref_delta = np.abs(ref - expected)
+            worst["ref_max_abs"] = max(worst["ref_max_abs"], float(ref_delta.max()))
+            worst["ref_sum_abs"] += float(ref_delta.sum())
+            worst["ref_n"] += ref_delta.size
+            ours_rows = np.abs(out[r : r + 1, :, :count].float().numpy().astype(np.float64) - expected)
+            worst.setdefault("ours_on_ref_rows", 0.0)
+            worst["ours_on_ref_rows"] += float(ours_rows.sum())
+    mean_abs = worst["sum_abs"] / worst["n"]
+    ref_mean = worst["ref_sum_abs"] / worst["ref_n"]
+    ours_mean_on_ref_rows = worst["ours_on_ref_rows"] / worst["ref_n"]
+    log(f"  errors vs float64 oracle: max_abs={worst['max_abs']:.3e} mean_abs={mean_abs:.3e}; "
+        f"bf16 reference path: max_abs={worst['ref_max_abs']:.3e} mean_abs={ref_mean:.3e}")
+    assert worst["max_abs"] <= MAX_ABS
+    assert mean_abs <= MEAN_ABS
+    assert ours_mean_on_ref_rows <= BF16_SLACK * ref_mean
+    assert worst["max_abs"] <= BF16_SLACK * worst["ref_max_abs"] or worst["max_abs"] <= 2 ** -8
+
+
+@torch.inference_mode()
+def test_step_is_deterministic(gpu_ops):
+    """Same inputs, same bits: the schedule depends only on lengths (cfg3, seed 0)."""
+    w = workloads.config(3, 0)
+    inputs = workloads.make_inputs(w)
+    log(f"determinism {w.name}")
+    first, _, _ = run_step(gpu_ops, w, inputs)
+    second, _, _ = run_step(gpu_ops, w, inputs)
+    assert torch.equal(first.view(torch.int16), second.view(torch.int16))

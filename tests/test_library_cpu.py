@@ -1,0 +1,169 @@
+"""CPU checks of libxinfer_attention_ops.so: exports, messages, validation, schemas, fakes.
+
+Nothing here launches a kernel: every C-ABI call below fails validation (or only
+queries a workspace size) before any HIP call, so these run without a GPU.
+"""
+
+import ctypes
+from pathlib import Path
+import re
+
+import pytest
+import torch
+from torch._subclasses.fake_tensor import FakeTensorMode
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+# Reference operator messages (compiler/common/kernels/attention.cpp).
+REFERENCE_MESSAGES = {
+    1: "Invalid Q/K/V shapes",                                              # :17-19
+    2: "Unsupported Q shape",                                               # :90-91
+    3: "Expected matching full-capacity K/V inputs [batch,kv_heads,capacity,head_dim]",  # :92-94
+    4: "Query heads must be a positive multiple of KV heads",               # :95-96
+    5: "Flash head dimension must be a multiple of 8 in 8..256",            # :97-98
+    6: "Invalid valid-prefix length",                                       # :102
+    7: "Attention scale must be finite and positive",                       # :103
+    8: "Cumulative lengths must start at zero",                             # :35
+    9: "Invalid query/KV lengths",                                          # :43-45
+}
+REFERENCE_SCHEMAS = {
+    # attention.cpp:129-134 and the triton_op schema inferred from kv_cache.py:45-52.
+    "batched_flash_attention": "xinfer::batched_flash_attention(Tensor q, Tensor k, Tensor v, Tensor offsets, "
+    "Tensor cuda_offsets, Tensor blocks, float scale) -> Tensor",
+    "flash_attention": "xinfer::flash_attention(Tensor q, Tensor k, Tensor v, Tensor kv_extent, float scale) -> Tensor",
+    "append_kv_batched": "xinfer::append_kv_batched(Tensor key, Tensor value, Tensor positions, Tensor cu_query, "
+    "Tensor(a4!) cache_key, Tensor(a5!) cache_value) -> ()",
+}
+
+
+class View4(ctypes.Structure):
+    _fields_ = [("data", ctypes.c_void_p), ("size", ctypes.c_int64 * 4), ("stride", ctypes.c_int64 * 4)]
+
+
+def view(sizes, strides=None, data=1 << 20):
+    if strides is None:
+        strides = [sizes[1] * sizes[2] * sizes[3], sizes[2] * sizes[3], sizes[3], 1]
+    return View4(data, (ctypes.c_int64 * 4)(*sizes), (ctypes.c_int64 * 4)(*strides))
+
+
+def declared_functions():
+    names = []
+    for header in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for match in re.finditer(r"\b([A-Za-z_]\w*)\s*\([^;{}]*\)\s*;", text):
+            names.append(match.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib(library_path):
+    torch.ops.load_library(str(library_path))  # resolves libtorch for the shim symbols
+    handle = ctypes.CDLL(str(library_path))
+    handle.xinfer_status_string.restype = ctypes.c_char_p
+    handle.xinfer_flash_attention_workspace_size.restype = ctypes.c_size_t
+    handle.xinfer_batched_flash_attention_workspace_size.restype = ctypes.c_size_t
+    return handle
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert {"xinfer_flash_attention", "xinfer_batched_flash_attention", "xinfer_append_kv_batched",
+            "aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
+            "aoti_torch_cuda_append_kv_batched"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
+
+
+def test_status_messages_match_the_reference(lib):
+    for code, message in REFERENCE_MESSAGES.items():
+        assert lib.xinfer_status_string(code).decode() == message
+
+
+def flash(lib, q, k, length, scale=0.1):
+    return lib.xinfer_flash_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k),
+                                      ctypes.c_int64(length), ctypes.c_double(scale),
+                                      ctypes.c_void_p(1 << 20), None, ctypes.c_size_t(0), None)
+
+
+def test_flash_validation_order_and_codes(lib):
+    q, k = view([1, 16, 2, 128]), view([1, 8, 64, 128])
+    assert flash(lib, view([1, 16, 513, 128]), k, 600) == 2
+    assert flash(lib, view([0, 16, 2, 128]), view([0, 8, 64, 128]), 5) == 2
+    assert flash(lib, q, view([2, 8, 64, 128]), 5) == 3
+    assert flash(lib, view([1, 12, 2, 128]), k, 5) == 4
+    assert flash(lib, view([1, 16, 2, 127]), view([1, 8, 64, 127]), 5) == 5
+    assert flash(lib, view([1, 16, 2, 264]), view([1, 8, 64, 264]), 5) == 5
+    for length in (0, 1, 65):
+        assert flash(lib, q, k, length) == 6
+    assert flash(lib, q, k, 5, scale=-1.0) == 7
+    assert flash(lib, q, k, 5, scale=float("inf")) == 7
+    strided = view([1, 16, 2, 128], [4096 * 2, 256 * 2, 2048 * 2, 2])
+    assert flash(lib, strided, k, 5) == 11
+
+
+def batched(lib, q, k, offsets, scale=0.1):
+    host = (ctypes.c_int32 * len(offsets))(*offsets)
+    return lib.xinfer_batched_flash_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), host,
+                                              ctypes.c_double(scale), ctypes.c_void_p(1 << 20), None,
+                                              ctypes.c_size_t(0), None)
+
+
+def test_batched_validation_codes(lib):
+    q, k = view([2, 16, 4, 128]), view([2, 8, 64, 128])
+    assert batched(lib, q, view([3, 8, 64, 128]), [0, 1, 2, 0, 5, 9]) == 1
+    assert batched(lib, q, k, [1, 1, 2, 0, 5, 9]) == 8
+    assert batched(lib, q, k, [0, 5, 6, 0, 5, 9]) == 9   # count > T
+    assert batched(lib, q, k, [0, 1, 2, 0, 0, 9]) == 9   # length < 1
+    assert batched(lib, q, k, [0, 3, 4, 0, 2, 9]) == 9   # length < count
+    assert batched(lib, q, k, [0, 1, 2, 0, 65, 70]) == 9  # length > capacity
+    assert batched(lib, q, k, [0, 1, 2, 0, 5, 9], scale=0.0) == 7
+
+
+def test_workspace_size_is_a_pure_host_query(lib):
+    q, k = view([8, 16, 1, 128]), view([8, 8, 16384, 128])
+    lengths = [13312, 2162, 386, 9459, 1399, 3852, 55, 182]
+    offsets = [0, 1, 2, 3, 4, 5, 6, 7, 8, 0]
+    for length in lengths:
+        offsets.append(offsets[-1] + length)
+    host = (ctypes.c_int32 * len(offsets))(*offsets)
+    bytes_ = lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(q), ctypes.byref(k), host)
+    assert bytes_ > 0
+    # One short row with one split needs no partial records.
+    q1, k1 = view([1, 16, 1, 128]), view([1, 8, 4096, 128])
+    assert lib.xinfer_flash_attention_workspace_size(ctypes.byref(q1), ctypes.byref(k1), ctypes.c_int64(100)) == 0
+
+
+def test_operator_schemas_tags_and_fakes(library_path):
+    from xinfer_amd.attention import attention_c_shims, cache_extent, load_attention_ops
+
+    load_attention_ops(library_path)
+    for name, schema in REFERENCE_SCHEMAS.items():
+        op = getattr(torch.ops.xinfer, name).default
+        assert str(op._schema) == schema
+    assert torch.Tag.flexible_layout in torch.ops.xinfer.flash_attention.default.tags
+    assert torch.Tag.flexible_layout in torch.ops.xinfer.batched_flash_attention.default.tags
+    shims = attention_c_shims()
+    assert len(shims) == 3
+    assert all(name in text[0] for name, text in zip(
+        ("aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
+         "aoti_torch_cuda_append_kv_batched"), shims.values()))
+    with FakeTensorMode(allow_non_fake_inputs=True):
+        q = torch.empty(2, 16, 3, 128, dtype=torch.bfloat16, device="cuda").transpose(1, 2).contiguous().transpose(1, 2)
+        k = torch.empty(2, 8, 64, 128, dtype=torch.bfloat16, device="cuda")
+        out = torch.ops.xinfer.flash_attention(q, k, k, cache_extent(10), 0.1)
+        assert out.shape == q.shape and out.is_contiguous() and out.device == q.device
+        offsets = torch.zeros(2, 3, dtype=torch.int32)
+        cuda_offsets = torch.empty(2, 3, dtype=torch.int32, device="cuda")
+        blocks = torch.empty(2, 1, dtype=torch.int32, device="cuda")
+        out = torch.ops.xinfer.batched_flash_attention(q, k, k, offsets, cuda_offsets, blocks, 0.1)
+        assert out.shape == q.shape and out.is_contiguous()
+        positions = torch.empty(2, 3, dtype=torch.long, device="cuda")
+        cu = torch.empty(3, dtype=torch.int32, device="cuda")
+        assert torch.ops.xinfer.append_kv_batched(k[:, :, :3], k[:, :, :3], positions, cu, k, k) is None
+        # The fake contract rejects what the native op rejects.
+        with pytest.raises(Exception):
+            torch.ops.xinfer.flash_attention(q[:, :3], k, k, cache_extent(10), 0.1)
+        with pytest.raises(Exception):
+            torch.ops.xinfer.batched_flash_attention(q, k, k, offsets[:, :2], cuda_offsets, blocks, 0.1)

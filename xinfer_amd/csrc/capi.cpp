@@ -1,0 +1,362 @@
+// C ABI of libxinfer_attention_ops.so: validation, work planning and launches.
+//
+// The planner turns host-side lengths into a static schedule carried in the
+// kernel arguments (kernel_args.h): rows with at most 8 query vectors per KV
+// head go to the split-KV decode kernel, the others to the MFMA prefill
+// kernel; rows whose keys are split get fp32 partial records in the caller's
+// workspace and a finalize pass.  The schedule is a function of the shapes
+// and lengths only, never of tensor data, so results are deterministic and
+// each row is isolated from the others' contents.
+#include <cmath>
+#include <cstdint>
+#include <vector>
+
+#include "../../include/xinfer_attention.h"
+#include "kernel_args.h"
+#include "launch.h"
+
+namespace xattn {
+namespace {
+
+constexpr int kDecodeMaxQueryVectors = 8;  // G * count at or below this: decode kernel
+constexpr int kPrefillTileQ = 128;         // query vectors per prefill work item
+constexpr int64_t kPrefillTargetItems = 256;
+constexpr int64_t kPrefillMinSplitKeys = 512;
+
+int padded_dim(int64_t d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
+int pow2_at_least(int x) {
+  int p = 1;
+  while (p < x) p <<= 1;
+  return p;
+}
+int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+struct Geometry {
+  int64_t B, Hq, Hkv, T, D, C;
+};
+
+bool attention_layout_ok(const xinfer_view4 &t) {
+  if (t.data == nullptr || (reinterpret_cast<uintptr_t>(t.data) & 15u) != 0) return false;
+  if (t.size[3] > 1 && t.stride[3] != 1) return false;
+  for (int i = 0; i < 3; ++i)
+    if (t.size[i] > 1 && (t.stride[i] % 8) != 0) return false;
+  return true;
+}
+
+View view_of(const xinfer_view4 &t) {
+  return View{static_cast<const uint16_t *>(t.data), t.stride[0], t.stride[1], t.stride[2]};
+}
+
+int check_heads_and_dim(const Geometry &g) {
+  if (g.Hq <= 0 || g.Hkv <= 0 || g.Hq % g.Hkv != 0) return XINFER_ERR_HEADS;
+  if (g.D < 8 || g.D > 256 || g.D % 8 != 0) return XINFER_ERR_HEAD_DIM;
+  return XINFER_OK;
+}
+
+struct Group {
+  int row0 = 0, nrows = 0;
+  AttnArgs dec{};
+  int dec_items = 0, dec_qr = 1;
+  AttnArgs pre{};
+  int pre_items = 0;
+  FinalizeArgs fin{};
+  bool need_finalize = false;
+};
+
+struct Plan {
+  std::vector<Group> groups;
+  int64_t records = 0;
+  int64_t D = 0;
+  size_t part_ml_offset() const { return (size_t)((records * D * 4 + 255) / 256 * 256); }
+  size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
+};
+
+// counts/lengths: per-row real queries and populated KV lengths (validated).
+Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts,
+               const std::vector<int32_t> &lengths) {
+  Plan plan;
+  plan.D = g.D;
+  const int G = (int)(g.Hq / g.Hkv);
+  const int dp = padded_dim(g.D);
+
+  // Keys per prefill split, chosen from the whole call's prefill work.
+  int64_t prefill_keys = 0;
+  for (int64_t r = 0; r < g.B; ++r) {
+    const int64_t qv = (int64_t)counts[r] * G;
+    if (qv > kDecodeMaxQueryVectors) prefill_keys += g.Hkv * ceil_div(qv, kPrefillTileQ) * lengths[r];
+  }
+  int64_t split_keys = ceil_div(ceil_div(prefill_keys, kPrefillTargetItems), 64) * 64;
+  if (split_keys < kPrefillMinSplitKeys) split_keys = kPrefillMinSplitKeys;
+
+  for (int64_t row0 = 0; row0 < g.B; row0 += kMaxRows) {
+    Group grp;
+    grp.row0 = (int)row0;
+    grp.nrows = (int)std::min<int64_t>(kMaxRows, g.B - row0);
+    int max_qv = 1;
+    for (int r = 0; r < grp.nrows; ++r) {
+      const int qv = counts[row0 + r] * G;
+      if (qv > 0 && qv <= kDecodeMaxQueryVectors) max_qv = std::max(max_qv, qv);
+    }
+    grp.dec_qr = pow2_at_least(max_qv);
+    const int tpi = decode_tokens_per_item(dp, grp.dec_qr);
+    grp.fin.nrows = grp.nrows;
+    grp.fin.row_base = grp.row0;
+    for (int r = 0; r < grp.nrows; ++r) {
+      const int64_t b = row0 + r;
+      const int cnt = counts[b], len = lengths[b];
+      const int qv = cnt * G;
+      FinalizeRow &fr = grp.fin.rows[r];
+      fr.count = cnt;
+      fr.nsplit = 0;
+      fr.rec_begin = 0;
+      if (cnt < g.T) grp.need_finalize = true;
+      if (cnt == 0) continue;
+      RowSched rs{};
+      rs.batch = (int32_t)b;
+      rs.count = cnt;
+      rs.length = len;
+      if (qv <= kDecodeMaxQueryVectors) {
+        rs.nsplit = (int32_t)ceil_div(len, tpi);
+        rs.ntiles = 1;
+        rs.item_begin = grp.dec_items;
+        grp.dec_items += (int)(g.Hkv * rs.nsplit);
+        grp.dec.rows[grp.dec.nrows++] = rs;
+      } else {
+        rs.ntiles = (int32_t)ceil_div(qv, kPrefillTileQ);
+        rs.nsplit = (int32_t)std::max<int64_t>(1, ceil_div(len, split_keys));
+        rs.item_begin = grp.pre_items;
+        grp.pre_items += (int)(g.Hkv * rs.ntiles * rs.nsplit);
+      }
+      if (rs.nsplit > 1) {
+        rs.rec_begin = plan.records;
+        plan.records += g.Hkv * rs.nsplit * (int64_t)qv;
+        grp.need_finalize = true;
+      }
+      if (qv <= kDecodeMaxQueryVectors)
+        grp.dec.rows[grp.dec.nrows - 1].rec_begin = rs.rec_begin;
+      else
+        grp.pre.rows[grp.pre.nrows++] = rs;
+      fr.nsplit = rs.nsplit;
+      fr.rec_begin = rs.rec_begin;
+    }
+    plan.groups.push_back(grp);
+  }
+  return plan;
+}
+
+int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const xinfer_view4 &k,
+             const xinfer_view4 &v, double scale, void *out, void *workspace, hipStream_t stream) {
+  const int G = (int)(g.Hq / g.Hkv);
+  const int dp = padded_dim(g.D);
+  float *part_o = static_cast<float *>(workspace);
+  float *part_ml =
+      plan.records ? reinterpret_cast<float *>(static_cast<char *>(workspace) + plan.part_ml_offset())
+                   : nullptr;
+  for (Group grp : plan.groups) {
+    for (AttnArgs *a : {&grp.dec, &grp.pre}) {
+      a->q = view_of(q);
+      a->k = view_of(k);
+      a->v = view_of(v);
+      a->out = static_cast<uint16_t *>(out);
+      a->o_sb = g.Hq * g.T * g.D;
+      a->o_sh = g.T * g.D;
+      a->o_st = g.D;
+      a->part_o = part_o;
+      a->part_ml = part_ml;
+      a->scale_log2 = (float)(scale * 1.4426950408889634);
+      a->D = (int32_t)g.D;
+      a->G = G;
+      a->Hkv = (int32_t)g.Hkv;
+    }
+    if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_items, stream) != hipSuccess)
+      return XINFER_ERR_LAUNCH;
+    if (grp.pre_items > 0 && launch_prefill(grp.pre, dp, grp.pre_items, stream) != hipSuccess)
+      return XINFER_ERR_LAUNCH;
+    if (grp.need_finalize) {
+      grp.fin.out = static_cast<uint16_t *>(out);
+      grp.fin.part_o = part_o;
+      grp.fin.part_ml = part_ml;
+      grp.fin.B = (int32_t)g.B;
+      grp.fin.Hq = (int32_t)g.Hq;
+      grp.fin.T = (int32_t)g.T;
+      grp.fin.D = (int32_t)g.D;
+      grp.fin.G = G;
+      if (launch_finalize(grp.fin, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
+    }
+  }
+  return XINFER_OK;
+}
+
+// Validation of xinfer::flash_attention (attention.cpp:84-104), in its order.
+int check_flash(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                int64_t valid_length, Geometry &g) {
+  if (!q || !k || !v) return XINFER_ERR_ARGUMENT;
+  g = Geometry{q->size[0], q->size[1], k->size[1], q->size[2], q->size[3], k->size[2]};
+  if (!(g.B > 0 && g.T >= 1 && g.T <= 512)) return XINFER_ERR_Q_SHAPE;
+  bool same = true;
+  for (int i = 0; i < 4; ++i) same = same && v->size[i] == k->size[i];
+  if (!(k->size[0] == g.B && g.C > 0 && k->size[3] == g.D && same)) return XINFER_ERR_KV_SHAPE;
+  if (int rc = check_heads_and_dim(g)) return rc;
+  if (!(valid_length >= g.T && valid_length <= g.C)) return XINFER_ERR_PREFIX;
+  return XINFER_OK;
+}
+
+// Validation of xinfer::batched_flash_attention (attention.cpp:17-45).
+int check_batched(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                  const int32_t *offsets, Geometry &g, std::vector<int32_t> &counts,
+                  std::vector<int32_t> &lengths) {
+  if (!q || !k || !v || !offsets) return XINFER_ERR_ARGUMENT;
+  g = Geometry{q->size[0], q->size[1], k->size[1], q->size[2], q->size[3], k->size[2]};
+  bool same = true;
+  for (int i = 0; i < 4; ++i) same = same && v->size[i] == k->size[i];
+  if (!(same && k->size[0] == g.B && k->size[3] == g.D) || g.B < 0 || g.T < 0)
+    return XINFER_ERR_QKV_SHAPES;
+  if (int rc = check_heads_and_dim(g)) return rc;
+  const int32_t *cuq = offsets, *cuk = offsets + g.B + 1;
+  if (cuq[0] != 0 || cuk[0] != 0) return XINFER_ERR_OFFSETS_START;
+  counts.resize(g.B);
+  lengths.resize(g.B);
+  for (int64_t r = 0; r < g.B; ++r) {
+    const int64_t count = (int64_t)cuq[r + 1] - cuq[r], length = (int64_t)cuk[r + 1] - cuk[r];
+    if (!(count >= 0 && count <= g.T && length >= count && length >= 1 && length <= g.C))
+      return XINFER_ERR_LENGTHS;
+    counts[r] = (int32_t)count;
+    lengths[r] = (int32_t)length;
+  }
+  return XINFER_OK;
+}
+
+int check_common(const xinfer_view4 &q, const xinfer_view4 &k, const xinfer_view4 &v, double scale) {
+  if (!(std::isfinite(scale) && scale > 0)) return XINFER_ERR_SCALE;
+  if (!attention_layout_ok(q) || !attention_layout_ok(k) || !attention_layout_ok(v))
+    return XINFER_ERR_LAYOUT;
+  return XINFER_OK;
+}
+
+}  // namespace
+}  // namespace xattn
+
+using namespace xattn;
+
+extern "C" {
+
+const char *xinfer_status_string(int status) {
+  switch (status) {
+    case XINFER_OK: return "Success";
+    case XINFER_ERR_QKV_SHAPES: return "Invalid Q/K/V shapes";
+    case XINFER_ERR_Q_SHAPE: return "Unsupported Q shape";
+    case XINFER_ERR_KV_SHAPE:
+      return "Expected matching full-capacity K/V inputs [batch,kv_heads,capacity,head_dim]";
+    case XINFER_ERR_HEADS: return "Query heads must be a positive multiple of KV heads";
+    case XINFER_ERR_HEAD_DIM: return "Flash head dimension must be a multiple of 8 in 8..256";
+    case XINFER_ERR_PREFIX: return "Invalid valid-prefix length";
+    case XINFER_ERR_SCALE: return "Attention scale must be finite and positive";
+    case XINFER_ERR_OFFSETS_START: return "Cumulative lengths must start at zero";
+    case XINFER_ERR_LENGTHS: return "Invalid query/KV lengths";
+    case XINFER_ERR_WORKSPACE: return "Attention workspace is smaller than its size query";
+    case XINFER_ERR_LAYOUT:
+      return "Attention tensors need a unit feature stride, strides divisible by 8 and 16-byte "
+             "aligned data";
+    case XINFER_ERR_CACHE:
+      return "Expected contiguous KV caches [batch,kv_heads,capacity,head_dim] matching key/value";
+    case XINFER_ERR_LAUNCH: return "HIP kernel launch failed";
+    case XINFER_ERR_ARGUMENT: return "Invalid argument";
+    default: return "Unknown xinfer status";
+  }
+}
+
+size_t xinfer_batched_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
+                                                     const int32_t *host_offsets) {
+  Geometry g;
+  std::vector<int32_t> counts, lengths;
+  if (check_batched(q, k, k, host_offsets, g, counts, lengths) != XINFER_OK) return 0;
+  return make_plan(g, counts, lengths).bytes();
+}
+
+int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
+                                   const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                   void *out, void *workspace, size_t workspace_bytes,
+                                   void *stream) {
+  Geometry g;
+  std::vector<int32_t> counts, lengths;
+  if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
+  if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (g.B == 0 || g.T == 0) return XINFER_OK;
+  if (out == nullptr) return XINFER_ERR_ARGUMENT;
+  const Plan plan = make_plan(g, counts, lengths);
+  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
+    return XINFER_ERR_WORKSPACE;
+  return run_plan(plan, g, *q, *k, *v, scale, out, workspace, static_cast<hipStream_t>(stream));
+}
+
+size_t xinfer_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
+                                             int64_t valid_length) {
+  Geometry g;
+  if (check_flash(q, k, k, valid_length, g) != XINFER_OK) return 0;
+  std::vector<int32_t> counts(g.B, (int32_t)g.T), lengths(g.B, (int32_t)valid_length);
+  return make_plan(g, counts, lengths).bytes();
+}
+
+int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                           int64_t valid_length, double scale, void *out, void *workspace,
+                           size_t workspace_bytes, void *stream) {
+  Geometry g;
+  if (int rc = check_flash(q, k, v, valid_length, g)) return rc;
+  if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (out == nullptr) return XINFER_ERR_ARGUMENT;
+  std::vector<int32_t> counts(g.B, (int32_t)g.T), lengths(g.B, (int32_t)valid_length);
+  const Plan plan = make_plan(g, counts, lengths);
+  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
+    return XINFER_ERR_WORKSPACE;
+  return run_plan(plan, g, *q, *k, *v, scale, out, workspace, static_cast<hipStream_t>(stream));
+}
+
+int xinfer_append_kv_batched(const xinfer_view4 *key, const xinfer_view4 *value,
+                             const int64_t *positions, int64_t pos_stride_b, int64_t pos_stride_t,
+                             const int32_t *cu_query, const xinfer_view4 *cache_key,
+                             const xinfer_view4 *cache_value, void *stream) {
+  if (!key || !value || !cache_key || !cache_value) return XINFER_ERR_ARGUMENT;
+  const int64_t B = key->size[0], H = key->size[1], T = key->size[2], D = key->size[3];
+  for (int i = 0; i < 4; ++i)
+    if (value->size[i] != key->size[i] || key->size[i] < 0) return XINFER_ERR_ARGUMENT;
+  if (B == 0 || H == 0 || T == 0 || D == 0) return XINFER_OK;
+  if (!positions || !cu_query || !key->data || !value->data) return XINFER_ERR_ARGUMENT;
+  for (const xinfer_view4 *c : {cache_key, cache_value}) {
+    if (!c->data || c->size[0] < B || c->size[1] != H || c->size[3] != D || c->size[2] <= 0)
+      return XINFER_ERR_CACHE;
+    if (c->stride[3] != 1 || c->stride[2] != D || c->stride[1] != c->size[2] * D ||
+        c->stride[0] != H * c->size[2] * D)
+      return XINFER_ERR_CACHE;
+    for (int i = 0; i < 4; ++i)
+      if (c->size[i] != cache_key->size[i]) return XINFER_ERR_CACHE;
+  }
+  AppendArgs a{};
+  a.key = view_of(*key);
+  a.value = view_of(*value);
+  a.key_sd = key->stride[3];
+  a.value_sd = value->stride[3];
+  a.positions = positions;
+  a.pos_sb = pos_stride_b;
+  a.pos_st = pos_stride_t;
+  a.cu_query = cu_query;
+  a.cache_key = static_cast<uint16_t *>(const_cast<void *>(cache_key->data));
+  a.cache_value = static_cast<uint16_t *>(const_cast<void *>(cache_value->data));
+  a.B = (int32_t)B;
+  a.H = (int32_t)H;
+  a.T = (int32_t)T;
+  a.D = (int32_t)D;
+  a.C = (int32_t)cache_key->size[2];
+  auto vec_ok = [&](const xinfer_view4 &t) {
+    if ((reinterpret_cast<uintptr_t>(t.data) & 15u) != 0 || t.stride[3] != 1 || D % 8 != 0) return false;
+    for (int i = 0; i < 3; ++i)
+      if (t.size[i] > 1 && t.stride[i] % 8 != 0) return false;
+    return true;
+  };
+  const bool vector = vec_ok(*key) && vec_ok(*value) &&
+                      (reinterpret_cast<uintptr_t>(cache_key->data) & 15u) == 0 &&
+                      (reinterpret_cast<uintptr_t>(cache_value->data) & 15u) == 0;
+  return launch_append(a, vector, static_cast<hipStream_t>(stream)) == hipSuccess ? XINFER_OK
+                                                                                  : XINFER_ERR_LAUNCH;
+}
+
+}  // extern "C"

@@ -1,0 +1,90 @@
+// Device-side helpers for the gfx950 (CDNA4) attention kernels: bf16 bit
+// conversions, 16-byte vector types, DPP row reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace xattn {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Round-to-nearest-even float -> bf16 bits (hardware conversion on gfx950).
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (__bf16)f);
+}
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+}
+
+__device__ __forceinline__ bf16x2 as_bf16x2(uint32_t w) { return __builtin_bit_cast(bf16x2, w); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
+
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+  return *reinterpret_cast<const u32x4 *>(p);
+}
+__device__ __forceinline__ void store16(uint16_t *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
+
+// 4-term bf16 dot product of two 8-element bf16 vectors accumulated in fp32.
+__device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a.x), as_bf16x2(b.x), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a.y), as_bf16x2(b.y), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a.z), as_bf16x2(b.z), acc, false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(as_bf16x2(a.w), as_bf16x2(b.w), acc, false);
+  return acc;
+}
+
+// DPP lane move within a 16-lane row (gfx9 encodings).
+template <int CTRL>
+__device__ __forceinline__ float dpp_move(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8-lane half row
+constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16-lane row
+
+// All-reduce (sum) over aligned groups of N lanes, N in {8,16,32,64}.  Every lane
+// of a group ends with the same value (each level adds a pair of equal partials).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp_move<kDppXor1>(x);
+  x += dpp_move<kDppXor2>(x);
+  x += dpp_move<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_move<kDppMirror>(x);
+  if constexpr (N >= 32) x += __shfl_xor(x, 16);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
+__device__ __forceinline__ float wave_max(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+  for (int m = 32; m >= 1; m >>= 1) x += __shfl_xor(x, m);
+  return x;
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Locate the row owning work item `item`: rows are sorted by item_begin.
+template <typename Row>
+__device__ __forceinline__ int find_row(const Row *rows, int nrows, int item) {
+  int r = 0;
+  for (int k = 1; k < nrows; ++k)
+    if (rows[k].item_begin <= item) r = k;
+  return r;
+}
+
+}  // namespace xattn

@@ -1,0 +1,70 @@
+// Kernel argument blocks shared by the host planner (capi.cpp) and the HIP
+// kernels.  Plain structs passed by value through the kernarg segment; the
+// per-row schedule travels inside them, so a launch needs no device metadata
+// and no host<->device copy.
+#pragma once
+
+#include <stdint.h>
+
+namespace xattn {
+
+// Rows per launch.  Callers with more rows are split into several launches.
+constexpr int kMaxRows = 64;
+
+// One batch row as seen by a kernel.
+struct RowSched {
+  int32_t batch;       // index into the batch dimension
+  int32_t count;       // real queries of this row (<= T)
+  int32_t length;      // populated KV length after the append (>= count, >= 1)
+  int32_t item_begin;  // first work item (blockIdx.x) of this row
+  int32_t nsplit;      // KV splits per (kv head[, query tile]); 1 = no merge
+  int32_t ntiles;      // query tiles per kv head (prefill); 1 for decode
+  int64_t rec_begin;   // first partial record of this row in the workspace
+};
+
+// Strided bf16 rank-4 tensor: element pointer + strides of dims 0..2 (dim 3 is unit).
+struct View {
+  const uint16_t *p;
+  int64_t sb, sh, st;
+};
+
+struct AttnArgs {
+  View q, k, v;
+  uint16_t *out;             // contiguous [B, Hq, T, D]
+  int64_t o_sb, o_sh, o_st;  // = Hq*T*D, T*D, D
+  float *part_o;             // [records][D] unnormalised fp32 partial outputs
+  float *part_ml;            // [records][2] (running max in log2 units, sum)
+  float scale_log2;          // softmax scale * log2(e)
+  int32_t D, G, Hkv;
+  int32_t nrows;
+  RowSched rows[kMaxRows];
+};
+
+// Finalize (merge split partials, zero padded queries) over all rows of a call.
+struct FinalizeRow {
+  int32_t count;
+  int32_t nsplit;     // > 1: row output is merged from partials
+  int64_t rec_begin;
+};
+
+struct FinalizeArgs {
+  uint16_t *out;
+  const float *part_o;
+  const float *part_ml;
+  int32_t B, Hq, T, D, G;
+  int32_t row_base;   // first batch index covered by this launch
+  int32_t nrows;
+  FinalizeRow rows[kMaxRows];
+};
+
+struct AppendArgs {
+  View key, value;
+  int64_t key_sd, value_sd;  // feature strides (1 on the vector path)
+  const int64_t *positions;
+  int64_t pos_sb, pos_st;
+  const int32_t *cu_query;
+  uint16_t *cache_key, *cache_value;  // contiguous [B, H, C, D]
+  int32_t B, H, T, D, C;
+};
+
+}  // namespace xattn

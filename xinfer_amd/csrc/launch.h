@@ -1,0 +1,21 @@
+// Host-side launchers of the HIP kernels (defined in the .hip files).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include "kernel_args.h"
+
+namespace xattn {
+
+hipError_t launch_append(const AppendArgs &a, bool vector, hipStream_t stream);
+
+// Keys handled by one decode work item for padded head dim `dp` and `qr` query
+// vectors per KV head (a power of two <= 8).
+int decode_tokens_per_item(int dp, int qr);
+hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int items, hipStream_t stream);
+
+hipError_t launch_prefill(const AttnArgs &a, int dp, int items, hipStream_t stream);
+
+hipError_t launch_finalize(const FinalizeArgs &a, hipStream_t stream);
+
+}  // namespace xattn
