@@ -336,7 +336,8 @@ def main():
     from xinfer_amd.attention import load_attention_ops
     from xinfer_amd.build import library_path
 
-    load_attention_ops(library_path())
+    # XINFER_ATTENTION_OPS_LIBRARY selects another build, as in the reference loader.
+    load_attention_ops(os.environ.get("XINFER_ATTENTION_OPS_LIBRARY") or library_path())
     with_cpu = not args.no_cpu_baseline
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)

@@ -4,14 +4,15 @@
 // kernel arguments (kernel_args.h): rows with at most 8 query vectors per KV
 // head go to the split-KV decode kernel, the others to the MFMA prefill
 // kernel; rows whose keys are split get fp32 partial records in the caller's
-// workspace and a finalize pass.  The schedule is a function of the shapes
-// and lengths only, never of tensor data, so results are deterministic and
-// each row is isolated from the others' contents.
+// workspace, combined by a merge launch after the attention kernels.  The
+// schedule is a function of the shapes and lengths only, never of tensor data,
+// so results are deterministic and each row is isolated from the others'
+// contents.
 #include <cmath>
 #include <cstdint>
 #include <vector>
 
-#include "../../include/xinfer_attention.h"
+#include "xinfer_attention.h"
 #include "kernel_args.h"
 #include "launch.h"
 
@@ -40,6 +41,8 @@ bool attention_layout_ok(const xinfer_view4 &t) {
   if (t.size[3] > 1 && t.stride[3] != 1) return false;
   for (int i = 0; i < 3; ++i)
     if (t.size[i] > 1 && (t.stride[i] % 8) != 0) return false;
+  // One (row, head) slice is addressed with 32-bit byte offsets.
+  if ((t.size[2] + 1) * t.stride[2] * 2 >= (int64_t(1) << 31)) return false;
   return true;
 }
 
@@ -59,8 +62,8 @@ struct Group {
   int dec_items = 0, dec_qr = 1;
   AttnArgs pre{};
   int pre_items = 0;
-  FinalizeArgs fin{};
-  bool need_finalize = false;
+  MergeArgs merge{};
+  int merge_items = 0, merge_max_splits = 0;
 };
 
 struct Plan {
@@ -72,8 +75,7 @@ struct Plan {
 };
 
 // counts/lengths: per-row real queries and populated KV lengths (validated).
-Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts,
-               const std::vector<int32_t> &lengths) {
+Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std::vector<int32_t> &lengths) {
   Plan plan;
   plan.D = g.D;
   const int G = (int)(g.Hq / g.Hkv);
@@ -99,28 +101,21 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts,
     }
     grp.dec_qr = pow2_at_least(max_qv);
     const int tpi = decode_tokens_per_item(dp, grp.dec_qr);
-    grp.fin.nrows = grp.nrows;
-    grp.fin.row_base = grp.row0;
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t b = row0 + r;
       const int cnt = counts[b], len = lengths[b];
-      const int qv = cnt * G;
-      FinalizeRow &fr = grp.fin.rows[r];
-      fr.count = cnt;
-      fr.nsplit = 0;
-      fr.rec_begin = 0;
-      if (cnt < g.T) grp.need_finalize = true;
-      if (cnt == 0) continue;
+      const int64_t qv = (int64_t)cnt * G;
       RowSched rs{};
       rs.batch = (int32_t)b;
       rs.count = cnt;
       rs.length = len;
-      if (qv <= kDecodeMaxQueryVectors) {
-        rs.nsplit = (int32_t)ceil_div(len, tpi);
-        rs.ntiles = 1;
+      rs.ntiles = 1;
+      rs.nsplit = 1;
+      const bool decode = qv <= kDecodeMaxQueryVectors;  // includes rows with no query (zero fill only)
+      if (decode) {
+        if (cnt > 0) rs.nsplit = (int32_t)ceil_div(len, tpi);
         rs.item_begin = grp.dec_items;
         grp.dec_items += (int)(g.Hkv * rs.nsplit);
-        grp.dec.rows[grp.dec.nrows++] = rs;
       } else {
         rs.ntiles = (int32_t)ceil_div(qv, kPrefillTileQ);
         rs.nsplit = (int32_t)std::max<int64_t>(1, ceil_div(len, split_keys));
@@ -129,15 +124,18 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts,
       }
       if (rs.nsplit > 1) {
         rs.rec_begin = plan.records;
-        plan.records += g.Hkv * rs.nsplit * (int64_t)qv;
-        grp.need_finalize = true;
+        plan.records += g.Hkv * rs.nsplit * qv;
+        MergeRow &mr = grp.merge.rows[grp.merge.nrows++];
+        mr.batch = (int32_t)b;
+        mr.count = cnt;
+        mr.nsplit = rs.nsplit;
+        mr.item_begin = grp.merge_items;
+        mr.rec_begin = rs.rec_begin;
+        grp.merge_items += (int)(g.Hkv * qv);
+        grp.merge_max_splits = std::max(grp.merge_max_splits, (int)rs.nsplit);
       }
-      if (qv <= kDecodeMaxQueryVectors)
-        grp.dec.rows[grp.dec.nrows - 1].rec_begin = rs.rec_begin;
-      else
-        grp.pre.rows[grp.pre.nrows++] = rs;
-      fr.nsplit = rs.nsplit;
-      fr.rec_begin = rs.rec_begin;
+      AttnArgs &a = decode ? grp.dec : grp.pre;
+      a.rows[a.nrows++] = rs;
     }
     plan.groups.push_back(grp);
   }
@@ -167,21 +165,26 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
       a->D = (int32_t)g.D;
       a->G = G;
       a->Hkv = (int32_t)g.Hkv;
+      a->T = (int32_t)g.T;
     }
+    grp.dec.total_items = grp.dec_items;
+    grp.pre.total_items = grp.pre_items;
     if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
     if (grp.pre_items > 0 && launch_prefill(grp.pre, dp, grp.pre_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
-    if (grp.need_finalize) {
-      grp.fin.out = static_cast<uint16_t *>(out);
-      grp.fin.part_o = part_o;
-      grp.fin.part_ml = part_ml;
-      grp.fin.B = (int32_t)g.B;
-      grp.fin.Hq = (int32_t)g.Hq;
-      grp.fin.T = (int32_t)g.T;
-      grp.fin.D = (int32_t)g.D;
-      grp.fin.G = G;
-      if (launch_finalize(grp.fin, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
+    if (grp.merge_items > 0) {
+      MergeArgs &m = grp.merge;
+      m.out = static_cast<uint16_t *>(out);
+      m.o_sb = g.Hq * g.T * g.D;
+      m.o_sh = g.T * g.D;
+      m.o_st = g.D;
+      m.part_o = part_o;
+      m.part_ml = part_ml;
+      m.D = (int32_t)g.D;
+      m.G = G;
+      m.total_items = grp.merge_items;
+      if (launch_merge(m, dp, grp.merge_max_splits, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
     }
   }
   return XINFER_OK;

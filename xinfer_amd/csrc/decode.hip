@@ -3,208 +3,290 @@
 //
 // Replaces, for those rows, the ATen FlashAttention-2 call of
 // compiler/common/kernels/attention.cpp:66-72 / :116-117.  Math: for every
-// query vector j of KV head h in row r,
-//   out_j = sum_t softmax_t(scale * q_j . k_t) v_t  over keys t <= L - count + i_j
+// query vector j = i*G + g of KV head h in row r,
+//   out_j = sum_t softmax_t(scale * q_j . k_t) v_t  over keys t <= L - count + i
 // (lower-right causal), fp32 scores / softmax / accumulation, bf16 in and out.
 //
-// Work item = (row, kv head, chunk of TOK_ITEM keys).  The chunk's K and V are
-// read exactly once from HBM and shared by the G grouped query heads.  A
-// 256-thread block = 4 waves; LPT = D/8 lanes hold one key row (16 bytes per
-// lane -> one 128-bit load), so a wave instruction reads TPW = 64/LPT whole
-// rows = 1 KB contiguous.  Each lane issues U loads of K then U of V before
-// any arithmetic, giving 2*U*16 B in flight per lane (128 KB per block at D=128).
-//   phase 1  scores: bf16 dot2 against the lane's 8 query features, reduced
-//            over the LPT lanes with DPP; stored to LDS.
-//   phase 2  per query vector: chunk max, p = exp2(s*scale*log2e - m), sum.
-//   phase 3  o += p * v from the registers loaded in the prologue; reduced over
-//            token slots (shuffles) and waves (LDS).
-// With one chunk the block writes normalised bf16 output; otherwise it writes
-// an fp32 partial record (o, m, l) that finalize.hip merges in a fixed order.
-// The schedule depends only on the lengths, so results are deterministic and
-// a row's output never depends on another row's data.
+// Work item = (row, kv head, chunk of TOK_ITEM keys); the chunk's K and V are
+// read from HBM exactly once and shared by the G grouped query heads.  One
+// block per item; every K/V load of the block (8 rows of 16 bytes per lane and
+// tensor for 2 query vectors) is issued before any arithmetic, and the small
+// register footprint keeps several blocks resident per CU, so the loads of
+// some blocks are in flight while others compute (measured on MI355X: 32 KB
+// per tensor per block is the read shape that sustains the most bandwidth).
+//
+// A block is 4 waves, each owning a contiguous quarter of the item.  LPT = D/8
+// lanes hold one key row (one 128-bit load per lane), so a wave instruction
+// reads TPW = 64/LPT whole rows (1 KB contiguous).  K and V are read with raw
+// buffer loads: the (row, head) base in scalar registers, a 32-bit lane offset
+// and a scalar per-row offset, so a load costs no vector address arithmetic;
+// the resource ends at the item's last key, and loads past it return zero
+// without touching memory.  Per block of U rows: bf16 dot2 against the lane's
+// 8 query features, a DPP all-reduce over the LPT lanes of a row, a block max
+// across the TPW row slots and an online-softmax update (running max m, sum l,
+// accumulator o), all lane-local.  The four waves are combined through LDS.
+//
+// One chunk per (row, head): the block writes normalised bf16 output.  Several
+// chunks: each writes an fp32 partial record per query vector, combined by
+// merge.hip.  The schedule depends only on the lengths, so results are
+// deterministic and a row's output never depends on another row's data.
+// Padded queries (t >= count) get zeros from the row's first item; a row with
+// count == 0 is scheduled only for that.
 #include "device_common.h"
 #include "kernel_args.h"
 
 namespace xattn {
 
-template <int DP, int QR, int U>
+template <int DP, int QR>
 struct DecodeShape {
-  static constexpr int LPT = DP / 8;        // lanes per key row
-  static constexpr int TPW = 64 / LPT;      // key rows per wave instruction
-  static constexpr int TOK_WAVE = TPW * U;  // keys per wave per item
-  static constexpr int TOK_ITEM = 4 * TOK_WAVE;
+  static constexpr int LPT = DP / 8;             // lanes per key row
+  static constexpr int TPW = 64 / LPT;           // key rows per wave instruction
+  static constexpr int U = QR <= 2 ? 4 : (QR == 4 ? 2 : 1);  // rows per lane per block
+  static constexpr int NB = 2;                   // blocks per wave per item
+  static constexpr int BLK = TPW * U;            // keys per wave block
+  static constexpr int TOK_WAVE = NB * BLK;      // keys per wave per item
+  static constexpr int TOK_ITEM = 4 * TOK_WAVE;  // keys per work item
 };
 
-template <int DP, int QR, int U>
-__global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
-  using S = DecodeShape<DP, QR, U>;
-  constexpr int LPT = S::LPT, TPW = S::TPW, TOK_WAVE = S::TOK_WAVE, TOK_ITEM = S::TOK_ITEM;
-  __shared__ float sc[QR][TOK_ITEM];
-  __shared__ float red[4][QR][DP];
-  __shared__ float stat_m[QR], stat_l[QR];
+struct DecodeItem {
+  int b, h, split, nsplit, cnt, L, t0, t1;
+  int64_t rec_begin;
+};
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  const int slot = lane / LPT, dc = lane % LPT;
-
-  const int item = blockIdx.x;
+__device__ __forceinline__ DecodeItem locate_item(const AttnArgs &a, int item, int tok_item) {
   const RowSched rs = a.rows[find_row(a.rows, a.nrows, item)];
+  DecodeItem it;
   const int local = item - rs.item_begin;
-  const int h = local / rs.nsplit, split = local - h * rs.nsplit;
-  const int b = rs.batch, L = rs.length, cnt = rs.count, G = a.G;
-  const int qrows = cnt * G;
-  const int t0 = split * TOK_ITEM;
-  const int t1 = min(L, t0 + TOK_ITEM);
-  const bool dact = dc * 8 < a.D;
+  it.h = local / rs.nsplit;
+  it.split = local - it.h * rs.nsplit;
+  it.nsplit = rs.nsplit;
+  it.b = rs.batch;
+  it.cnt = rs.count;
+  it.L = rs.length;
+  it.t0 = it.split * tok_item;
+  it.t1 = min(it.L, it.t0 + tok_item);
+  it.rec_begin = rs.rec_begin;
+  return it;
+}
 
-  // Query features of this lane's 8-wide slice, for every query vector j = i*G + g.
-  u32x4 qv[QR];
+// Registers of one in-flight item: its K/V rows and query features.
+template <int DP, int QR>
+struct DecodeRegs {
+  using S = DecodeShape<DP, QR>;
+  u32x4 k[S::NB][S::U], v[S::NB][S::U], q[QR];
+};
+
+// Zero out[b, h*G + g, t, :] for g < G and t in [t_begin, T).
+__device__ __forceinline__ void zero_queries(const AttnArgs &a, int b, int h, int t_begin) {
+  const int per_head = (a.T - t_begin) * a.D / 8;  // 16-byte chunks per head
+  for (int idx = threadIdx.x; idx < a.G * per_head; idx += blockDim.x) {
+    const int g = idx / per_head, rest = idx - g * per_head;
+    uint16_t *dst = a.out + b * a.o_sb + (int64_t)(h * a.G + g) * a.o_sh + (int64_t)t_begin * a.o_st;
+    store16(dst + rest * 8, u32x4{0, 0, 0, 0});
+  }
+}
+
+// Query features of the item's vectors (clamped into the row; zeroed past D later).
+template <int DP, int QR>
+__device__ __forceinline__ void load_query(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r, int dc) {
+  const int qrows = it.cnt * a.G;
+  const int dcc = dc * 8 < a.D ? dc : a.D / 8 - 1;
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
-    qv[j] = u32x4{0, 0, 0, 0};
-    if (j < qrows && dact) {
-      const int g = j % G, i = j / G;
-      qv[j] = load16(a.q.p + b * a.q.sb + (int64_t)(h * G + g) * a.q.sh + (int64_t)i * a.q.st + dc * 8);
-    }
+    const int jc = j < qrows ? j : qrows - 1;
+    r.q[j] = load16(a.q.p + it.b * a.q.sb + (int64_t)(it.h * a.G + jc % a.G) * a.q.sh +
+                    (int64_t)(jc / a.G) * a.q.st + dcc * 8);
+  }
+}
+
+// Issue every load of an item: K/V rows through buffer resources ending at the
+// item's last key, and the query features (clamped into the row, zeroed past D).
+template <int DP, int QR>
+__device__ __forceinline__ void issue_item(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
+                                           int wave, int slot, int dc) {
+  using S = DecodeShape<DP, QR>;
+  if (it.cnt == 0) return;
+  // The query first: its loads complete before the K/V rows the first dot needs.
+  if constexpr (QR <= 4) load_query(a, it, r, dc);  // wider groups load it in process_item
+  const uint32_t row_bytes_k = (uint32_t)(a.k.st * 2), row_bytes_v = (uint32_t)(a.v.st * 2);
+  const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
+  const auto rv = buffer_rsrc(a.v.p + it.b * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
+  const int first = it.t0 + wave * S::TOK_WAVE + slot;  // this lane's first key row
+  const uint32_t vk = (uint32_t)first * row_bytes_k + dc * 16, vv = (uint32_t)first * row_bytes_v + dc * 16;
+#pragma unroll
+  for (int nb = 0; nb < S::NB; ++nb) {
+#pragma unroll
+    for (int u = 0; u < S::U; ++u) r.k[nb][u] = buffer_load16(rk, vk, (nb * S::BLK + u * S::TPW) * row_bytes_k);
+#pragma unroll
+    for (int u = 0; u < S::U; ++u) r.v[nb][u] = buffer_load16(rv, vv, (nb * S::BLK + u * S::TPW) * row_bytes_v);
+  }
+}
+
+template <int DP, int QR>
+struct DecodeShared {
+  float red_o[4][QR][DP];
+  float red_m[4][QR], red_l[4][QR];
+};
+
+// Compute one item from its registers; writes output or partial records.
+template <int DP, int QR>
+__device__ __forceinline__ void process_item(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
+                                             DecodeShared<DP, QR> &sh, int wave, int lane, int slot, int dc) {
+  using S = DecodeShape<DP, QR>;
+  constexpr int LPT = S::LPT, TPW = S::TPW, U = S::U, NB = S::NB, BLK = S::BLK;
+  const int tid = threadIdx.x, G = a.G;
+  if (it.cnt == 0) {
+    zero_queries(a, it.b, it.h, 0);
+    return;
+  }
+  if (it.split == 0 && it.cnt < a.T) zero_queries(a, it.b, it.h, it.cnt);
+  if constexpr (QR > 4) load_query(a, it, r, dc);
+  const int qrows = it.cnt * G;
+  const float c = a.scale_log2;
+  const int wb = it.t0 + wave * S::TOK_WAVE;
+  const int we = min(it.t1, wb + S::TOK_WAVE);
+  const bool dact = dc * 8 < a.D;
+  int lim[QR];
+#pragma unroll
+  for (int j = 0; j < QR; ++j) {
+    lim[j] = j < qrows ? it.L - it.cnt + j / G : -1;  // last visible key of query vector j
+    if (!(j < qrows && dact)) r.q[j] = u32x4{0, 0, 0, 0};
   }
 
-  // Issue every K and V load of this lane up front.  Keys >= t1 are never read.
-  const uint16_t *kbase = a.k.p + b * a.k.sb + (int64_t)h * a.k.sh + dc * 8;
-  const uint16_t *vbase = a.v.p + b * a.v.sb + (int64_t)h * a.v.sh + dc * 8;
-  const int wt0 = t0 + wave * TOK_WAVE + slot;
-  u32x4 kr[U], vr[U];
+  float m[QR], l[QR], acc[QR][8];
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int tok = wt0 + u * TPW;
-    kr[u] = (tok < t1 && dact) ? load16(kbase + (int64_t)tok * a.k.st) : u32x4{0, 0, 0, 0};
-  }
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int tok = wt0 + u * TPW;
-    vr[u] = (tok < t1 && dact) ? load16(vbase + (int64_t)tok * a.v.st) : u32x4{0, 0, 0, 0};
-  }
-
-  // Phase 1: raw scores q_j . k_t.
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int tok = wt0 + u * TPW;
-#pragma unroll
-    for (int j = 0; j < QR; ++j) {
-      float d = group_sum<LPT>(dot8_bf16(kr[u], qv[j], 0.0f));
-      if (dc == 0 && tok < t1) sc[j][tok - t0] = d;
-    }
-  }
-  __syncthreads();
-
-  // Phase 2: chunk softmax statistics, one wave per query vector.
-  const int n = t1 - t0;
-  for (int j = wave; j < QR; j += 4) {
-    if (j >= qrows) continue;
-    const int lim = L - cnt + j / G;  // last visible key of this query
-    float mx = -INFINITY;
-    for (int t = lane; t < n; t += 64)
-      if (t0 + t <= lim) mx = fmaxf(mx, sc[j][t]);
-    mx = wave_max(mx);
-    const float ms = mx * a.scale_log2;
-    float sum = 0.0f;
-    for (int t = lane; t < n; t += 64) {
-      const float p = (t0 + t <= lim && mx != -INFINITY) ? fast_exp2(fmaf(sc[j][t], a.scale_log2, -ms)) : 0.0f;
-      sc[j][t] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      stat_m[j] = ms;
-      stat_l[j] = sum;
-    }
-  }
-  __syncthreads();
-
-  // Phase 3: o_j += p_jt * v_t over this lane's keys.
-  float acc[QR][8];
-#pragma unroll
-  for (int j = 0; j < QR; ++j)
+  for (int j = 0; j < QR; ++j) {
+    m[j] = -INFINITY;
+    l[j] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+  }
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int tok = wt0 + u * TPW;
-    if (tok < t1) {
-      const u32x4 w = vr[u];
-      const float v8[8] = {bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y),
-                           bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+  for (int nb = 0; nb < NB; ++nb) {
+    float p[QR][U], alpha[QR];
+#pragma unroll
+    for (int j = 0; j < QR; ++j) {
+      float mb = -INFINITY;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tok = wb + nb * BLK + u * TPW + slot;
+        const float s = group_sum<LPT>(dot8_bf16(r.k[nb][u], r.q[j], 0.0f));
+        p[j][u] = (tok < we && tok <= lim[j]) ? s : -INFINITY;
+        mb = fmaxf(mb, p[j][u]);
+      }
+      mb = slot_max<LPT>(mb);
+      const float mn = fmaxf(m[j], mb * c);
+      const float mu = mn == -INFINITY ? 0.0f : mn;
+      alpha[j] = fast_exp2(m[j] - mu);
+      float ps = 0.0f;
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        p[j][u] = fast_exp2(fmaf(p[j][u], c, -mu));
+        ps += p[j][u];
+      }
+      l[j] = fmaf(l[j], alpha[j], ps);
+      m[j] = mn;
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float vf[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const uint32_t w = r.v[nb][u][e >> 1];
+        vf[u] = (e & 1) ? bf16_hi(w) : bf16_lo(w);
+      }
 #pragma unroll
       for (int j = 0; j < QR; ++j) {
-        const float p = sc[j][tok - t0];
+        float t = acc[j][e] * alpha[j];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] = fmaf(p, v8[e], acc[j][e]);
+        for (int u = 0; u < U; ++u) t = fmaf(p[j][u], vf[u], t);
+        acc[j][e] = t;
       }
     }
   }
-  // Reduce over the TPW token slots of the wave (lanes dc, dc+LPT, ...).
+
+  // Sum over the TPW row slots of the wave (the max m is already wave-uniform).
 #pragma unroll
-  for (int j = 0; j < QR; ++j)
+  for (int j = 0; j < QR; ++j) {
+    l[j] = slot_sum<LPT>(l[j]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = acc[j][e];
-#pragma unroll
-      for (int m = LPT; m < 64; m <<= 1) x += __shfl_xor(x, m);
-      acc[j][e] = x;
-    }
+    for (int e = 0; e < 8; ++e) acc[j][e] = slot_sum<LPT>(acc[j][e]);
+  }
   if (slot == 0 && dact) {
 #pragma unroll
     for (int j = 0; j < QR; ++j)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red[wave][j][dc * 8 + e] = acc[j][e];
+      for (int e = 0; e < 8; ++e) sh.red_o[wave][j][dc * 8 + e] = acc[j][e];
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int j = 0; j < QR; ++j) {
+      sh.red_m[wave][j] = m[j];
+      sh.red_l[wave][j] = l[j];
+    }
   }
   __syncthreads();
 
-  // Combine the 4 waves; write output or a partial record.
+  // Combine the four waves, then write the output or a partial record.
   for (int idx = tid; idx < QR * DP; idx += 256) {
     const int j = idx / DP, d = idx % DP;
     if (j >= qrows || d >= a.D) continue;
-    const float o = (red[0][j][d] + red[1][j][d]) + (red[2][j][d] + red[3][j][d]);
-    if (rs.nsplit == 1) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, sh.red_m[w][j]);
+    const float mu = mx == -INFINITY ? 0.0f : mx;
+    float o = 0.0f, lsum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      const float wt = fast_exp2(sh.red_m[w][j] - mu);
+      o = fmaf(wt, sh.red_o[w][j][d], o);
+      lsum = fmaf(wt, sh.red_l[w][j], lsum);
+    }
+    if (it.nsplit == 1) {
       const int g = j % G, i = j / G;
-      uint16_t *dst = a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)i * a.o_st;
-      dst[d] = (uint16_t)f32_to_bf16_bits(o / stat_l[j]);
+      uint16_t *dst = a.out + it.b * a.o_sb + (int64_t)(it.h * G + g) * a.o_sh + (int64_t)i * a.o_st;
+      dst[d] = (uint16_t)f32_to_bf16_bits(o / lsum);
     } else {
-      const int64_t rec = rs.rec_begin + ((int64_t)h * rs.nsplit + split) * qrows + j;
+      const int64_t rec = it.rec_begin + ((int64_t)it.h * it.nsplit + it.split) * qrows + j;
       a.part_o[rec * a.D + d] = o;
-      if (d == 0) {
-        a.part_ml[2 * rec] = stat_m[j];
-        a.part_ml[2 * rec + 1] = stat_l[j];
-      }
+      if (d == 0) *reinterpret_cast<u32x2 *>(a.part_ml + 2 * rec) = u32x2{__float_as_uint(mx), __float_as_uint(lsum)};
     }
   }
 }
 
-int decode_tokens_per_item(int dp, int qr) {
-  const int u = qr <= 2 ? 16 : (qr <= 4 ? 8 : 4);
-  return 4 * (64 / (dp / 8)) * u;
+template <int DP, int QR>
+__global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
+  using S = DecodeShape<DP, QR>;
+  __shared__ DecodeShared<DP, QR> sh;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int slot = lane / S::LPT, dc = lane % S::LPT;
+  const DecodeItem it = locate_item(a, blockIdx.x, S::TOK_ITEM);
+  DecodeRegs<DP, QR> r;
+  issue_item(a, it, r, wave, slot, dc);
+  process_item(a, it, r, sh, wave, lane, slot, dc);
 }
 
-template <int DP, int QR>
-static hipError_t launch_decode_q(const AttnArgs &a, int items, hipStream_t stream) {
-  constexpr int U = QR <= 2 ? 16 : (QR <= 4 ? 8 : 4);
-  hipLaunchKernelGGL((decode_kernel<DP, QR, U>), dim3(items), dim3(256), 0, stream, a);
-  return hipGetLastError();
+int decode_tokens_per_item(int dp, int qr) {
+  const int u = qr <= 2 ? 4 : (qr == 4 ? 2 : 1);
+  return 4 * 2 * (64 / (dp / 8)) * u;
 }
 
 template <int DP>
-static hipError_t launch_decode_d(const AttnArgs &a, int qr, int items, hipStream_t stream) {
+static hipError_t launch_decode_d(const AttnArgs &a, int qr, int blocks, hipStream_t stream) {
   switch (qr) {
-    case 1: return launch_decode_q<DP, 1>(a, items, stream);
-    case 2: return launch_decode_q<DP, 2>(a, items, stream);
-    case 4: return launch_decode_q<DP, 4>(a, items, stream);
-    default: return launch_decode_q<DP, 8>(a, items, stream);
+    case 1: hipLaunchKernelGGL((decode_kernel<DP, 1>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<DP, 2>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<DP, 4>), dim3(blocks), dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<DP, 8>), dim3(blocks), dim3(256), 0, stream, a); break;
   }
+  return hipGetLastError();
 }
 
-hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int items, hipStream_t stream) {
+hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int blocks, hipStream_t stream) {
   switch (dp) {
-    case 64: return launch_decode_d<64>(a, qr, items, stream);
-    case 128: return launch_decode_d<128>(a, qr, items, stream);
-    default: return launch_decode_d<256>(a, qr, items, stream);
+    case 64: return launch_decode_d<64>(a, qr, blocks, stream);
+    case 128: return launch_decode_d<128>(a, qr, blocks, stream);
+    default: return launch_decode_d<256>(a, qr, blocks, stream);
   }
 }
 

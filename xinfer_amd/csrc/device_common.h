@@ -67,6 +67,45 @@ __device__ __forceinline__ float group_sum(float x) {
   return x;
 }
 
+// All-reduce over lanes {l, l ^ 16} / {l, l ^ 32} with the gfx950 permlane
+// swaps.  A swap of x with itself returns x's even-row (lower-half) and
+// odd-row (upper-half) copies in its two results; their sum / max is the
+// reduction over the pair on every lane, in the same order on both lanes.
+__device__ __forceinline__ float pair_sum16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_sum32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float pair_max16(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_max32(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i + 8) mod 16 within each row
+
+// Reductions over the lanes l, l + S, l + 2S, ... (S = stride, a power of two
+// >= 8): the key-row slots of a wave in the decode kernel.
+template <int S>
+__device__ __forceinline__ float slot_sum(float x) {
+  if constexpr (S <= 8) x += dpp_move<kDppRowRor8>(x);
+  if constexpr (S <= 16) x = pair_sum16(x);
+  if constexpr (S <= 32) x = pair_sum32(x);
+  return x;
+}
+template <int S>
+__device__ __forceinline__ float slot_max(float x) {
+  if constexpr (S <= 8) x = fmaxf(x, dpp_move<kDppRowRor8>(x));
+  if constexpr (S <= 16) x = pair_max16(x);
+  if constexpr (S <= 32) x = pair_max32(x);
+  return x;
+}
+
 __device__ __forceinline__ float wave_max(float x) {
   for (int m = 32; m >= 1; m >>= 1) x = fmaxf(x, __shfl_xor(x, m));
   return x;
@@ -77,6 +116,18 @@ __device__ __forceinline__ float wave_sum(float x) {
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Raw buffer resource over [base, base + bytes): the 64-bit base lives in
+// scalar registers and loads take a 32-bit lane offset plus a scalar offset.
+// Range checking makes a load at or past `bytes` return zero without a
+// memory access.  0x00020000 is the descriptor's fourth dword on the gfx9
+// family (32-bit data format, no swizzle).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buffer_load16(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 0));
+}
 
 // Locate the row owning work item `item`: rows are sorted by item_begin.
 template <typename Row>

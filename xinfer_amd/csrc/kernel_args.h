@@ -13,15 +13,14 @@ constexpr int kMaxRows = 64;
 
 // One batch row as seen by a kernel.
 struct RowSched {
-  int32_t batch;       // index into the batch dimension
-  int32_t count;       // real queries of this row (<= T)
-  int32_t length;      // populated KV length after the append (>= count, >= 1)
-  int32_t item_begin;  // first work item (blockIdx.x) of this row
-  int32_t nsplit;      // KV splits per (kv head[, query tile]); 1 = no merge
-  int32_t ntiles;      // query tiles per kv head (prefill); 1 for decode
-  int64_t rec_begin;   // first partial record of this row in the workspace
+  int32_t batch;        // index into the batch dimension
+  int32_t count;        // real queries of this row (<= T); 0 = only zero its output
+  int32_t length;       // populated KV length after the append (>= count, >= 1)
+  int32_t item_begin;   // first work item (blockIdx.x) of this row
+  int32_t nsplit;       // KV splits per group; 1 = no partial records
+  int32_t ntiles;       // query tiles per kv head (prefill); 1 for decode
+  int64_t rec_begin;    // first partial record of this row in the workspace
 };
-
 // Strided bf16 rank-4 tensor: element pointer + strides of dims 0..2 (dim 3 is unit).
 struct View {
   const uint16_t *p;
@@ -35,26 +34,30 @@ struct AttnArgs {
   float *part_o;             // [records][D] unnormalised fp32 partial outputs
   float *part_ml;            // [records][2] (running max in log2 units, sum)
   float scale_log2;          // softmax scale * log2(e)
-  int32_t D, G, Hkv;
+  int32_t D, G, Hkv, T;
+  int32_t total_items;       // work items of this launch (the decode grid may be smaller)
   int32_t nrows;
   RowSched rows[kMaxRows];
 };
 
-// Finalize (merge split partials, zero padded queries) over all rows of a call.
-struct FinalizeRow {
-  int32_t count;
-  int32_t nsplit;     // > 1: row output is merged from partials
-  int64_t rec_begin;
+// Merge of split partial records (merge.hip): one work item per query vector.
+struct MergeRow {
+  int32_t batch;
+  int32_t count;       // real queries of the row
+  int32_t nsplit;      // records per query vector (> 1)
+  int32_t item_begin;  // first merge work item (blockIdx.x) of this row
+  int64_t rec_begin;   // first partial record of the row
 };
 
-struct FinalizeArgs {
+struct MergeArgs {
   uint16_t *out;
+  int64_t o_sb, o_sh, o_st;
   const float *part_o;
   const float *part_ml;
-  int32_t B, Hq, T, D, G;
-  int32_t row_base;   // first batch index covered by this launch
+  int32_t D, G;
+  int32_t total_items;  // query vectors to merge
   int32_t nrows;
-  FinalizeRow rows[kMaxRows];
+  MergeRow rows[kMaxRows];
 };
 
 struct AppendArgs {

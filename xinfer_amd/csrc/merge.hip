@@ -1,0 +1,119 @@
+// Merge of split-KV partial records into the bf16 output.
+//
+// When the keys of a group of query vectors are split over several work
+// items, each item writes, per query vector, an fp32 record: unnormalised
+// output o[D] and the pair (m, l) -- running max in log2 units and sum.  This
+// kernel combines the records of one query vector:
+//   M = max_s m_s,  w_s = exp2(m_s - M),  out = sum_s w_s o_s / sum_s w_s l_s
+// Each thread folds its share of the splits with an online rescale (running
+// max, sum and accumulator), in increasing split order; thread states are then
+// folded in a fixed order, so the result is deterministic.  Splits that saw no
+// visible key carry m = -inf and weight 0.  Running as its own launch, it reads
+// the records after the producing kernel has completed, which orders them
+// without any device-scope fence inside the attention kernels.
+//
+// A block is VPB query vectors x SG split lanes x FC feature lanes (4
+// features each): with few splits per vector (prefill) a 256-thread block has
+// SG = 1, one thread owning a vector's 4 features across all splits; with many
+// splits (long decode rows) one 256-thread block per vector spreads them over
+// SG = 256 / FC split lanes.
+#include "device_common.h"
+#include "kernel_args.h"
+
+namespace xattn {
+
+struct MergeState {
+  float m, l;
+  f32x4 o;
+};
+
+__device__ __forceinline__ void fold(MergeState &st, float ms, float ls, f32x4 os) {
+  if (ms == -INFINITY) return;
+  const float mn = fmaxf(st.m, ms);
+  const float a = fast_exp2(st.m - mn), w = fast_exp2(ms - mn);  // st.m = -inf -> a = 0
+  st.l = st.l * a + ls * w;
+  st.o.x = st.o.x * a + os.x * w;
+  st.o.y = st.o.y * a + os.y * w;
+  st.o.z = st.o.z * a + os.z * w;
+  st.o.w = st.o.w * a + os.w * w;
+  st.m = mn;
+}
+
+template <int DP, int SG, int THREADS>
+__global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
+  constexpr int FC = DP / 4;                // feature lanes
+  constexpr int VPB = THREADS / (FC * SG);  // query vectors per block
+  __shared__ MergeState red[SG > 1 ? SG : 1][SG > 1 ? FC : 1];
+
+  const int tid = threadIdx.x, f = tid % FC, sg = (tid / FC) % SG, vl = tid / (FC * SG);
+  const int vec = blockIdx.x * VPB + vl;
+  const bool vvalid = vec < a.total_items;
+  const MergeRow mr = a.rows[find_row(a.rows, a.nrows, vvalid ? vec : 0)];
+  const int local = vec - mr.item_begin;
+  const int qrows = mr.count * a.G;
+  const int h = local / qrows, j = local - h * qrows;
+  const int64_t rec0 = mr.rec_begin + (int64_t)h * mr.nsplit * qrows + j;
+  const int d = f * 4;
+
+  MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  if (vvalid && d < a.D) {
+    int s = sg;
+    for (; s + 3 * SG < mr.nsplit; s += 4 * SG) {  // four records in flight
+      u32x2 ml[4];
+      f32x4 o[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t rec = rec0 + (int64_t)(s + u * SG) * qrows;
+        ml[u] = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * rec);
+        o[u] = *reinterpret_cast<const f32x4 *>(a.part_o + rec * a.D + d);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
+    }
+    for (; s < mr.nsplit; s += SG) {
+      const int64_t rec = rec0 + (int64_t)s * qrows;
+      const u32x2 ml = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * rec);
+      fold(st, __uint_as_float(ml.x), __uint_as_float(ml.y), *reinterpret_cast<const f32x4 *>(a.part_o + rec * a.D + d));
+    }
+  }
+  if constexpr (SG > 1) {
+    red[sg][f] = st;
+    __syncthreads();
+    if (sg != 0) return;
+    for (int k = 1; k < SG; ++k) {
+      const MergeState other = red[k][f];
+      fold(st, other.m, other.l, other.o);
+    }
+  }
+  if (!vvalid || d >= a.D) return;
+  const float inv = 1.0f / st.l;
+  const int g = j % a.G, i = j / a.G;
+  uint16_t *dst = a.out + mr.batch * a.o_sb + (int64_t)(h * a.G + g) * a.o_sh + (int64_t)i * a.o_st;
+  *reinterpret_cast<u32x2 *>(dst + d) =
+      u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
+}
+
+// Splits at or below this count use one thread per (vector, 4 features).
+constexpr int kMergeSerialSplits = 8;
+
+template <int DP>
+static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t stream) {
+  constexpr int FC = DP / 4;
+  if (max_splits <= kMergeSerialSplits) {
+    constexpr int VPB = 256 / FC;
+    hipLaunchKernelGGL((merge_kernel<DP, 1, 256>), dim3((a.total_items + VPB - 1) / VPB), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), dim3(a.total_items), dim3(256), 0, stream, a);
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream) {
+  switch (dp) {
+    case 64: return launch_merge_d<64>(a, max_splits, stream);
+    case 128: return launch_merge_d<128>(a, max_splits, stream);
+    default: return launch_merge_d<256>(a, max_splits, stream);
+  }
+}
+
+}  // namespace xattn

@@ -17,8 +17,8 @@
 
 #include <cmath>
 
-#include "../../include/xinfer_attention.h"
-#include "../../include/xinfer_attention_aoti.h"
+#include "xinfer_attention.h"
+#include "xinfer_attention_aoti.h"
 
 namespace xinfer {
 namespace {
@@ -40,6 +40,8 @@ bool kernel_layout(const at::Tensor &t) {
   if (t.size(3) > 1 && t.stride(3) != 1) return false;
   for (int i = 0; i < 3; ++i)
     if (t.size(i) > 1 && t.stride(i) % 8 != 0) return false;
+  // One (row, head) slice is addressed with 32-bit byte offsets.
+  if ((t.size(2) + 1) * t.stride(2) * 2 >= (int64_t(1) << 31)) return false;
   return true;
 }
 

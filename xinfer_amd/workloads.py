@@ -133,8 +133,8 @@ def make_inputs(w: Workload):
 
     Returns dict(q [B,Hq,T,D], k/v caches [B,Hkv,C,D], new_k/new_v [B,Hkv,T,D],
     positions int64 [B,T] (padded tokens point past the capacity and are never
-    read), counts, lengths).  The new tokens are already written into the caches'
-    copies ``k_after``/``v_after`` (the populated state the attention reads).
+    read), counts, lengths).  ``k_after``/``v_after`` are the caches the attention
+    reads: with the new tokens written in when the step appends, else the caches.
     """
     import torch
 
@@ -159,9 +159,10 @@ def make_inputs(w: Workload):
     for r, (n, p) in enumerate(zip(w.counts, w.prefixes)):
         positions[r, :n] = torch.arange(p, p + n)
     k_after, v_after = k.clone(), v.clone()
-    for r, (n, p) in enumerate(zip(w.counts, w.prefixes)):
-        k_after[r, :, p:p + n] = new_k[r, :, :n]
-        v_after[r, :, p:p + n] = new_v[r, :, :n]
+    if w.append:
+        for r, (n, p) in enumerate(zip(w.counts, w.prefixes)):
+            k_after[r, :, p:p + n] = new_k[r, :, :n]
+            v_after[r, :, p:p + n] = new_v[r, :, :n]
     return dict(q=q, k=k, v=v, new_k=new_k, new_v=new_v, positions=positions,
                 k_after=k_after, v_after=v_after,
                 counts=list(w.counts), lengths=list(w.lengths))
