@@ -30,6 +30,8 @@ SDPA on bf16 tensors (the reference CPU path), both with thread counts.
 from __future__ import annotations
 
 import argparse
+import csv
+import hashlib
 import json
 import os
 from pathlib import Path
@@ -43,10 +45,92 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2516.6
 MALL_BYTES = 256 << 20
 METRIC = "decode attn KV GB/s (% HBM peak) + prefill TFLOP/s (% MFMA), bs 1–8 ragged"
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
+KERNEL_SOURCES = ("xinfer_amd/csrc/*.hip", "xinfer_amd/csrc/*.h", "xinfer_amd/csrc/*.cpp")
 
 
 def log(message):
     print(message, file=sys.stderr, flush=True)
+
+
+def sources_digest():
+    """Digest of the native sources: a traffic record only applies to the kernels it measured."""
+    digest = hashlib.sha256()
+    for pattern in KERNEL_SOURCES:
+        for path in sorted(ROOT.glob(pattern)):
+            digest.update(path.name.encode())
+            digest.update(path.read_bytes())
+    return digest.hexdigest()[:16]
+
+
+def dominant_kernel(w):
+    """Name of the kernel that carries the workload's algorithmic work.
+
+    Mirrors the library's kernel choice: head dims pad to 64 / 128 / 256; prefill
+    uses two key halves (8 waves) at 128; decode is instantiated for the
+    power-of-two query vectors per KV head (count * G).
+    """
+    dp = 64 if w.dim <= 64 else (128 if w.dim <= 128 else 256)
+    if w.kind == "prefill":
+        return f"void xattn::prefill_kernel<{dp}, {2 if dp == 128 else 1}>(xattn::AttnArgs)"
+    qv = max(1, max(c for c in w.counts) * (w.heads // w.kv_heads))
+    qr = 1
+    while qr < qv:
+        qr *= 2
+    return f"void xattn::decode_kernel<{dp}, {qr}>(xattn::AttnArgs)"
+
+
+def record_traffic(fetch_csv, write_csv):
+    """Turn two rocprofv3 --pmc passes (FETCH_SIZE, WRITE_SIZE) into TRAFFIC_FILE.
+
+    Each pass ran ``bench.py --eager --copy-probe``.  The probe's elementwise
+    copy moves exactly COPY_PROBE_BYTES each way, which calibrates the counter
+    readings (KiB per dispatch) to bytes; every kernel's average reading is then
+    scaled by the same factor.
+    """
+    def per_kernel(path, counter):
+        sums = {}
+        with open(path, newline="") as handle:
+            for row in csv.DictReader(handle):
+                if row["Counter_Name"] != counter:
+                    continue
+                entry = sums.setdefault(row["Kernel_Name"], [0.0, 0])
+                entry[0] += float(row["Counter_Value"])
+                entry[1] += 1
+        return {name: total / count for name, (total, count) in sums.items()}
+
+    record = {"sources": sources_digest(), "copy_probe_bytes": COPY_PROBE_BYTES, "kernels": {}}
+    for counter, path in (("FETCH_SIZE", fetch_csv), ("WRITE_SIZE", write_csv)):
+        averages = per_kernel(path, counter)
+        probes = [name for name in averages if "neg_kernel" in name]
+        if len(probes) != 1:
+            raise SystemExit(f"{path}: no unique copy-probe dispatch for {counter}")
+        scale = COPY_PROBE_BYTES / (averages[probes[0]] * 1024)
+        record[counter.lower() + "_scale"] = scale
+        for name, kib in averages.items():
+            if name.startswith("void xattn::"):
+                entry = record["kernels"].setdefault(name, {})
+                entry[counter.lower() + "_kib"] = kib
+                entry[counter.lower() + "_bytes"] = kib * 1024 * scale
+    for entry in record["kernels"].values():
+        entry["bytes"] = entry.get("fetch_size_bytes", 0.0) + entry.get("write_size_bytes", 0.0)
+    TRAFFIC_FILE.write_text(json.dumps(record, indent=1) + "\n")
+    print(json.dumps(record, indent=1))
+
+
+def measured_traffic(w):
+    """HBM bytes per launch of the dominant kernel from TRAFFIC_FILE, or None.
+
+    None when no record exists or when it was taken on other kernel sources.
+    """
+    try:
+        record = json.loads(TRAFFIC_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if record.get("sources") != sources_digest():
+        return None
+    entry = record.get("kernels", {}).get(dominant_kernel(w))
+    return None if entry is None else entry["bytes"]
 
 
 class Runner:
@@ -273,12 +357,14 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
         "cache_copies": runner.copies,
         "roofline": {
             "bound": "hbm" if decode else "mfma",
-            "kernel": "decode_kernel + finalize_kernel" if decode else "prefill_kernel + finalize_kernel",
+            "kernel": dominant_kernel(w),
+            "timed": "one attention op: the kernel above plus its split merge",
             "achieved": achieved,
             "peak": peak,
             "unit": unit,
             "frac": achieved / peak,
-            "traffic": None,
+            "traffic": measured_traffic(w),
+            "traffic_unit": "B per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, copy-calibrated)",
             "algorithmic_per_launch": work,
         },
         "config": w.summary(),
@@ -313,6 +399,29 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
     return result
 
 
+COPY_PROBE_BYTES = 256 << 20
+
+
+def copy_probe():
+    """Three elementwise copies (dst = -src) of COPY_PROBE_BYTES between two device buffers.
+
+    An elementwise kernel rather than copy_, which may go to a DMA engine.  Each
+    launch reads and writes exactly COPY_PROBE_BYTES, so the ratio of that to the
+    kernel's FETCH_SIZE / WRITE_SIZE counter readings scales the attention
+    kernels' readings to bytes.
+    """
+    import torch
+
+    src = torch.ones(COPY_PROBE_BYTES // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        torch.neg(src, out=dst)
+    torch.cuda.synchronize()
+    log(f"[bench] copy probe: 3 x {COPY_PROBE_BYTES} B elementwise copies")
+    del src, dst
+    torch.cuda.empty_cache()
+
+
 def main():
     parser = argparse.ArgumentParser(description="xinfer attention hot-path benchmark (one MI355X)")
     parser.add_argument("--gpus", type=int, default=1)
@@ -322,7 +431,16 @@ def main():
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
+    parser.add_argument("--record-traffic", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                        help="write the HBM traffic record from two rocprofv3 --pmc counter_collection "
+                             "CSVs (FETCH_SIZE, WRITE_SIZE) and exit; no GPU needed")
+    parser.add_argument("--copy-probe", action="store_true",
+                        help="first run a plain 256 MiB device copy: the known-size kernel that calibrates "
+                             "rocprofv3 FETCH_SIZE / WRITE_SIZE counters")
     args = parser.parse_args()
+    if args.record_traffic:
+        record_traffic(*args.record_traffic)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
               "The attention operator would shard by rows or KV heads with no exchange; see DESIGN.md.",
@@ -338,6 +456,8 @@ def main():
 
     # XINFER_ATTENTION_OPS_LIBRARY selects another build, as in the reference loader.
     load_attention_ops(os.environ.get("XINFER_ATTENTION_OPS_LIBRARY") or library_path())
+    if args.copy_probe:
+        copy_probe()
     with_cpu = not args.no_cpu_baseline
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
