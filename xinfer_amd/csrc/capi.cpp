@@ -46,6 +46,12 @@ bool attention_layout_ok(const xinfer_view4 &t) {
   return true;
 }
 
+// The prefill kernel addresses one batch row of Q ([Hq, T, D]) with 32-bit
+// byte offsets from the row's first head.
+bool query_layout_ok(const xinfer_view4 &q) {
+  return (q.size[1] * q.stride[1] + q.size[2] * q.stride[2]) * 2 < (int64_t(1) << 31);
+}
+
 View view_of(const xinfer_view4 &t) {
   return View{static_cast<const uint16_t *>(t.data), t.stride[0], t.stride[1], t.stride[2]};
 }
@@ -231,7 +237,8 @@ int check_batched(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
 
 int check_common(const xinfer_view4 &q, const xinfer_view4 &k, const xinfer_view4 &v, double scale) {
   if (!(std::isfinite(scale) && scale > 0)) return XINFER_ERR_SCALE;
-  if (!attention_layout_ok(q) || !attention_layout_ok(k) || !attention_layout_ok(v))
+  if (!attention_layout_ok(q) || !query_layout_ok(q) || !attention_layout_ok(k) ||
+      !attention_layout_ok(v))
     return XINFER_ERR_LAYOUT;
   return XINFER_OK;
 }

@@ -5,28 +5,43 @@
 // :116-117.  Same math as decode.hip: lower-right causal softmax(scale*QK^T)V
 // over the populated prefix, fp32 softmax state, bf16 in/out.
 //
-// Work item = (row, kv head, tile of 128 query vectors, KV split).  The query
+// Work item = (row, kv head, key split, tile of 128 query vectors).  The query
 // vectors of one KV head are enumerated j = i*G + g (query i, grouped head g),
 // so one tile serves all G heads that share the K/V tile in LDS.
 //
-// Waves: four query groups of 32 vectors x KH key halves.  With KH = 2 (head
-// dim 128) a block is 8 waves, two per SIMD, so one wave's MFMAs overlap the
-// other's softmax; wave w+4 takes keys 32..63 of every 64-key tile and is
-// merged into wave w at the end.  Each wave computes the transposed problem
-// with v_mfma_f32_32x32x16_bf16:
+// Waves: four query groups of 32 vectors x KH key slices.  With KH = 2 (head
+// dims 64 and 128) a block is 8 waves, two per SIMD, so one wave's MFMAs
+// overlap the other's softmax; wave w+4 takes keys 32..63 of every 64-key
+// tile and is folded into wave w at the end.  Each wave computes the
+// transposed problem with v_mfma_f32_32x32x16_bf16:
 //   S^T[key, j]  = K[key, :] . Q[j, :]      A = K tile (LDS), B = Q^T (registers)
-//   O^T[d, j]   += V^T[d, key] P^T[key, j]  A = V^T tile (LDS), B = P^T (from S^T)
+//   O^T[d, j]   += V^T[d, key] P^T[key, j]  A = V^T (LDS, transposing reads), B = P^T
 // so a lane's accumulator column is one query vector: the online-softmax max /
 // sum are per lane (plus one exchange with lane^32) and the S^T accumulator
-// registers are directly the PV B operand.  K is staged row-major, V transposed
-// ([d][key]); the next tile's global loads are issued into registers before the
-// current tile is computed and stored to LDS after it.
+// registers are directly the PV B operand.
+//
+// K/V tiles travel HBM -> LDS without registers: buffer_load_dwordx4 ... lds
+// writes each lane's 16 bytes at M0 + 16 * lane, so every load instruction
+// fills one contiguous 1 KB block, and the lanes choose which 16-byte chunks of
+// the tile they fetch.  That choice implements an XOR swizzle of the chunks of
+// each key row (against LDS bank conflicts) with no address arithmetic on the
+// store side.  NST tiles are in flight: while tile t is computed, the loads of
+// tiles t+1 .. t+NST-1 are outstanding, with one barrier per tile.
+//
+// V is kept row-major ([key][d]) and read with ds_read_b64_tr_b16, which
+// transposes 4x16 blocks of 16-bit elements within each 16-lane group: lane j
+// supplies the address of V[k0 + j/4][d0 + 4(j%4) .. +3] and receives
+// V[k0 .. k0+3][d0 + j], i.e. four consecutive keys of one feature, which is
+// the A-operand layout of the PV product.
 //
 // MFMA 32x32x16 lane layout used (A: 32xK16, B: K16x32, C: 32x32):
 //   A lane l: row l%32, k = 8*(l/32) + 0..7      B lane l: col l%32, same k
 //   C lane l, reg r: row 8*(r/4) + 4*(l/32) + r%4, col l%32
-// The PV product contracts over keys; the key <-> k-slot assignment only has to
-// agree between the A and B operands, and both are derived from the C layout.
+//
+// Softmax rescaling is lazy: a column's running max m only moves when a tile's
+// max exceeds it by more than kRescaleSlack (log2 units), so most tiles skip
+// the accumulator rescale.  Weights exp2(s - m) then stay below 2^kRescaleSlack;
+// O and the normaliser use the same m, so the quotient is unchanged.
 //
 // Several splits of a tile write fp32 partial records, combined by merge.hip.
 // The tile-0 / split-0 item zeroes the row's padded queries (t >= count).
@@ -37,9 +52,65 @@ namespace xattn {
 
 constexpr int kTileQ = 128;  // query vectors per work item
 constexpr int kBN = 64;      // keys per LDS tile
+constexpr float kRescaleSlack = 8.0f;
+
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
 
 __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Transposing 8-byte LDS read (see the header comment for the lane mapping).
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t *p) {
+  const shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) shortx4 *)(p));
+  return __builtin_bit_cast(u32x2, r);
+}
+
+// One 16-byte-per-lane buffer load into LDS: lane i's 16 bytes land at LDS
+// byte address m0 + 16 * i.  Written as inline asm so that the compiler does
+// not track these loads: it would otherwise wait for all of them before any
+// transposing LDS read, which would drain the load pipeline every tile.  The
+// waits for them are explicit (wait_loads_and_barrier); loads the compiler
+// does track are unaffected, since extra outstanding loads only make its own
+// waits stricter.
+__device__ __forceinline__ void lds_load16(u32x4 rsrc, uint32_t lds_byte, uint32_t voffset, uint32_t soffset) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_byte)), "v"(voffset), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soffset))
+               : "memory", "m0");
+}
+
+// Buffer descriptor words for [base, base + bytes) (raw buffer, no stride;
+// loads past `bytes` return zero).
+__device__ __forceinline__ u32x4 buffer_words(const void *base, uint32_t bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+__device__ __forceinline__ uint32_t lds_address(const uint16_t *p) {
+  return (uint32_t)(uintptr_t)(lds_void *)(p);
+}
+
+// Wait until at most N vector-memory operations of this wave are outstanding
+// (loads return in issue order), then synchronise the block.  The empty asm
+// keeps the compiler from moving LDS accesses across the barrier.
+template <int N>
+__device__ __forceinline__ void wait_loads_and_barrier() {
+  static_assert(N >= 0 && N < 16, "vmcnt field");
+  // s_waitcnt encoding (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14].
+  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Wait for this wave's LDS reads, then synchronise the block.
+__device__ __forceinline__ void wait_lds_and_barrier() {
+  __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Key range [ks0, ks1) of split `split` for a tile whose last visible key is kend-1.
@@ -52,37 +123,53 @@ __device__ __forceinline__ void split_range(int kend, int nsplit, int split, int
 template <int DP, int KH>
 struct PrefillShape {
   static constexpr int THREADS = 256 * KH;
-  static constexpr int KP = DP + 8;   // K tile pitch (bf16); 16-byte pad against bank conflicts
-  static constexpr int VP = kBN + 8;  // V^T tile pitch
-  static constexpr int NDS = DP / 16; // k-steps of the QK product
-  static constexpr int NDT = DP / 32; // 32-row d tiles of the output
-  static constexpr int KCH = kBN * (DP / 8) / THREADS;        // K 16-byte chunks per thread
-  static constexpr int VCH = (kBN / 2) * (DP / 8) / THREADS;  // V key-pair chunks per thread
+  static constexpr int NDS = DP / 16;                 // k-steps of the QK product
+  static constexpr int NDT = DP / 32;                 // 32-row d tiles of the output
+  static constexpr int CHUNKS = DP / 8;               // 16-byte chunks per key row
+  static constexpr int TILE = kBN * DP;               // bf16 elements of one K (or V) tile
+  static constexpr int LOADS = kBN * CHUNKS / THREADS;  // 16-byte loads per thread per K (or V) tile
+  static constexpr int NST = 4 * TILE * 3 <= 100 * 1024 ? 3 : 2;  // tiles in flight (K+V: 4*TILE bytes)
+  static constexpr int KPW = kBN / KH;                // keys of each tile per wave
+  static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
+  static constexpr int FOLD = KH > 1 ? 4 * (NDT * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
+  static constexpr int SMEM = (NST * 4 * TILE > FOLD ? NST * 4 * TILE : FOLD);
 };
+
+// XOR swizzles of the 16-byte chunks of a key row (chunk c of key k is stored
+// at slot c ^ swz(k)).  K: a K read takes chunk c of 32 consecutive keys, so
+// the 16 keys served together land in 16 different slots.  V: a transposing
+// read takes two adjacent chunks of 4 consecutive keys (k0 % 4 == 0), which
+// land in disjoint slot pairs.
+template <int CHUNKS>
+__device__ __forceinline__ int k_swizzle(int key) { return key & (CHUNKS >= 16 ? 15 : CHUNKS - 1); }
+template <int CHUNKS>
+__device__ __forceinline__ int v_swizzle(int key) { return (2 * (key & 3)) & (CHUNKS - 1); }
 
 template <int DP, int KH>
 __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   using S = PrefillShape<DP, KH>;
-  constexpr int THREADS = S::THREADS, KP = S::KP, VP = S::VP, NDS = S::NDS, NDT = S::NDT;
-  constexpr int KCH = S::KCH, VCH = S::VCH;
-  constexpr int KEYS_PER_WAVE = kBN / KH;  // keys of each tile this wave owns
-  constexpr int NKT = KEYS_PER_WAVE / 32;  // 32-key sub-tiles per wave per tile
-  static_assert(KCH >= 1 && VCH >= 1, "tile staging needs at least one chunk per thread");
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[kBN * KP];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[DP * VP];
-  __shared__ float xchg[KH > 1 ? 4 : 1][KH > 1 ? NDT * 16 + 2 : 1][64];
+  constexpr int THREADS = S::THREADS, NDS = S::NDS, NDT = S::NDT, CHUNKS = S::CHUNKS;
+  constexpr int TILE = S::TILE, LOADS = S::LOADS, NST = S::NST, KPW = S::KPW, NKT = S::NKT;
+  static_assert(LOADS >= 1 && kBN * CHUNKS == LOADS * THREADS, "tile = whole load instructions");
+  __shared__ __attribute__((aligned(16))) uint16_t smem[S::SMEM / 2];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
   const int qgroup = wave & 3, khalf = wave >> 2;
 
-  const int item = blockIdx.x;
+  // The hardware hands consecutive blocks to the 8 XCDs in turn.  Block b runs
+  // item (b % 8) * (grid / 8) + b / 8, so each XCD gets a contiguous run of
+  // items; items are ordered (row, head, split, tile), so the tiles that read
+  // the same keys share that XCD's L2.
+  const int nblocks = gridDim.x;
+  const int item = (int)(blockIdx.x % 8) * (nblocks / 8) + (int)(blockIdx.x / 8);
+  if (item >= a.total_items) return;
   const RowSched rs = a.rows[find_row(a.rows, a.nrows, item)];
   const int local = item - rs.item_begin;
   const int per_head = rs.ntiles * rs.nsplit;
   const int h = local / per_head;
-  const int tile = (local - h * per_head) / rs.nsplit;
-  const int split = local - h * per_head - tile * rs.nsplit;
+  const int split = (local - h * per_head) / rs.ntiles;
+  const int tile = local - h * per_head - split * rs.ntiles;
   const int b = rs.batch, L = rs.length, cnt = rs.count, G = a.G, D = a.D;
   const int qrows = cnt * G, p0 = L - cnt;
 
@@ -100,32 +187,82 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int kend = p0 + j_last / G + 1;
   int ks0, ks1;
   split_range(kend, rs.nsplit, split, ks0, ks1);
+  const int ntile = (ks1 - ks0 + kBN - 1) / kBN;
 
   // This lane's query vector.
   const int j = tile * kTileQ + qgroup * 32 + col;
   const bool jvalid = j < qrows;
   const int g = j % G, qi = j / G;
-  const int lim = p0 + qi;  // last visible key
+  const int lim = min(p0 + qi, ks1 - 1);  // last key this column may see in this split
   const int jw_first = tile * kTileQ + qgroup * 32;
   const bool wave_active = jw_first < qrows;
   const int wave_kmax = p0 + (min(jw_first + 31, qrows - 1)) / G;  // last key any column sees
   const int wave_kmin = p0 + jw_first / G;                          // last key of the first column
 
-  // Loads are unconditional, from addresses clamped into the valid range (last
-  // query vector, last key of the split, last feature chunk), so they issue
-  // without branches.  Clamped query features are zeroed; clamped keys are
-  // masked on the scores; clamped features past D only meet zero query
-  // features or land in output rows >= D, which are never stored.
-  bf16x8 qf[NDS];
-  {
-    const int jc = jvalid ? j : qrows - 1;
-    const uint16_t *qp = a.q.p + b * a.q.sb + (int64_t)(h * G + jc % G) * a.q.sh + (int64_t)(jc / G) * a.q.st;
-    u32x4 raw[NDS];
+  // Tile loads.  Buffer descriptors end at the split's last key, so the rows
+  // of a partial last tile read as zero (and are masked on the scores).  Load
+  // i of this thread fills 16-byte slot q = (wave * LOADS + i) * 64 + lane of
+  // the tile: key q / CHUNKS, slot q % CHUNKS, holding chunk slot ^ swizzle.
+  // Chunks past D (padded head dims) repeat the row's last chunk: finite
+  // values that only meet zero query features or unused output rows.
+  const uint32_t k_row = (uint32_t)a.k.st * 2, v_row = (uint32_t)a.v.st * 2;
+  const u32x4 k_rsrc = buffer_words(a.k.p + b * a.k.sb + (int64_t)h * a.k.sh, (uint32_t)ks1 * k_row);
+  const u32x4 v_rsrc = buffer_words(a.v.p + b * a.v.sb + (int64_t)h * a.v.sh, (uint32_t)ks1 * v_row);
+  uint32_t k_voff[LOADS], v_voff[LOADS];
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds) raw[ds] = load16(qp + min(ds * 16 + half * 8, D - 8));
+  for (int i = 0; i < LOADS; ++i) {
+    const int q = (wave * LOADS + i) * 64 + lane;
+    const int key = q / CHUNKS, slot = q % CHUNKS;
+    k_voff[i] = key * k_row + (uint32_t)min(slot ^ k_swizzle<CHUNKS>(key), D / 8 - 1) * 16;
+    v_voff[i] = key * v_row + (uint32_t)min(slot ^ v_swizzle<CHUNKS>(key), D / 8 - 1) * 16;
+  }
+  // The query tile goes through LDS the same way, into the last stage's
+  // buffer, ahead of the first tiles: row jr = j - tile*kTileQ of the tile
+  // holds query vector j, swizzled like K.  Rows past the tile's queries and
+  // features past D load as zero (an offset past the descriptor's range).
+  constexpr int QLOADS = kTileQ * CHUNKS / THREADS;
+  static_assert(kTileQ * CHUNKS == QLOADS * THREADS && kTileQ * DP <= 2 * TILE, "query tile fits a stage");
+  auto issue_query = [&]() {
+    const u32x4 q_rsrc = buffer_words(a.q.p + b * a.q.sb + (int64_t)(h * G) * a.q.sh, 0x7fffffffu);
+    uint16_t *qdst = smem + (NST - 1) * 2 * TILE;
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds)
-      qf[ds] = as_bf16x8((jvalid && ds * 16 + half * 8 < D) ? raw[ds] : u32x4{0, 0, 0, 0});
+    for (int i = 0; i < QLOADS; ++i) {
+      const int qs = (wave * QLOADS + i) * 64 + lane;
+      const int jr = qs / CHUNKS, chunk = (qs % CHUNKS) ^ k_swizzle<CHUNKS>(jr);
+      const int jq = tile * kTileQ + jr;
+      const uint32_t off = (jq < qrows && chunk < D / 8)
+                               ? (uint32_t)(((jq % G) * a.q.sh + (jq / G) * a.q.st) * 2 + chunk * 16)
+                               : 0x80000000u;
+      lds_load16(q_rsrc, lds_address(qdst + (wave * QLOADS + i) * 512), off, 0);
+    }
+  };
+  auto issue = [&](int stage, int kb) {
+    uint16_t *kdst = smem + stage * 2 * TILE, *vdst = kdst + TILE;
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      lds_load16(k_rsrc, lds_address(kdst + (wave * LOADS + i) * 512), k_voff[i], (uint32_t)kb * k_row);
+#pragma unroll
+    for (int i = 0; i < LOADS; ++i)
+      lds_load16(v_rsrc, lds_address(vdst + (wave * LOADS + i) * 512), v_voff[i], (uint32_t)kb * v_row);
+  };
+
+  // LDS read offsets (elements) of this lane, fixed for the whole item.
+  // K (A operand of QK): key kl = khalf*KPW + 32kt + col, chunk 2ds + half.
+  // Q (B operand, read once): row jr = qgroup*32 + col, same chunks.
+  const int kl0 = khalf * KPW + col, jr0 = qgroup * 32 + col;
+  int k_off[NDS];
+#pragma unroll
+  for (int ds = 0; ds < NDS; ++ds) k_off[ds] = kl0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(kl0)) * 8);
+  // V (A operand of PV) for d tile t: 16-lane group gq = lane/16, jj = lane%16
+  // addresses key kv0 (+16hh +8 for the second read) and features
+  // 32t + 16(gq%2) + 4(jj%4); kv0 % 4 == jj / 4 for every read.
+  const int gq = lane >> 4, jj = lane & 15;
+  const int kv0 = khalf * KPW + 4 * (gq >> 1) + (jj >> 2);
+  int v_off[NDT];
+#pragma unroll
+  for (int t = 0; t < NDT; ++t) {
+    const int dch = 4 * t + 2 * (gq & 1) + ((jj & 3) >> 1);
+    v_off[t] = kv0 * DP + ((dch ^ v_swizzle<CHUNKS>(kv0)) * 8) + 4 * (jj & 1);
   }
 
   f32x16 acc[NDT];
@@ -135,145 +272,130 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
   const float c = a.scale_log2;
+  const bf16x2 ones = as_bf16x2(0x3f803f80u);
 
-  const uint16_t *kbase = a.k.p + b * a.k.sb + (int64_t)h * a.k.sh;
-  const uint16_t *vbase = a.v.p + b * a.v.sb + (int64_t)h * a.v.sh;
-
-  // Register staging of one tile: K chunks (key, 8 features) and V key pairs.
-  u32x4 kst[KCH], vst0[VCH], vst1[VCH];
-  auto load_tile = [&](int kb) {
+  bf16x8 qf[NDS];  // Q^T B operands, read from LDS at tile 0
+  auto compute = [&](int stage, int kb) {
+    const uint16_t *Kt = smem + stage * 2 * TILE, *Vt = Kt + TILE;
+    const int kw = kb + khalf * KPW;  // first key of this wave's share
+    if (!(wave_active && kw <= wave_kmax && kw < ks1)) return;
+    f32x16 s[NKT];
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int cidx = tid + i * THREADS;
-      const int key = cidx / (DP / 8), dcc = min(cidx % (DP / 8), D / 8 - 1);
-      const int tok = min(kb + key, ks1 - 1);
-      kst[i] = load16(kbase + (int64_t)tok * a.k.st + dcc * 8);
-    }
+    for (int kt = 0; kt < NKT; ++kt) {
 #pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int cidx = tid + i * THREADS;
-      const int kp = cidx % (kBN / 2), dcc = min(cidx / (kBN / 2), D / 8 - 1);
-      const int tok0 = min(kb + 2 * kp, ks1 - 1), tok1 = min(kb + 2 * kp + 1, ks1 - 1);
-      vst0[i] = load16(vbase + (int64_t)tok0 * a.v.st + dcc * 8);
-      vst1[i] = load16(vbase + (int64_t)tok1 * a.v.st + dcc * 8);
-    }
-  };
-  auto store_tile = [&]() {
+      for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < KCH; ++i) {
-      const int cidx = tid + i * THREADS;
-      const int key = cidx / (DP / 8), dcc = cidx % (DP / 8);
-      store16(&Ks[key * KP + dcc * 8], kst[i]);
-    }
-#pragma unroll
-    for (int i = 0; i < VCH; ++i) {
-      const int cidx = tid + i * THREADS;
-      const int kp = cidx % (kBN / 2), dcc = cidx / (kBN / 2);
-      const u32x4 v0 = vst0[i], v1 = vst1[i];
-      uint32_t *dst = reinterpret_cast<uint32_t *>(&Vt[(dcc * 8) * VP + 2 * kp]);
-      constexpr int row32 = VP / 2;
-      dst[0 * row32] = (v0.x & 0xffffu) | (v1.x << 16);
-      dst[1 * row32] = (v0.x >> 16) | (v1.x & 0xffff0000u);
-      dst[2 * row32] = (v0.y & 0xffffu) | (v1.y << 16);
-      dst[3 * row32] = (v0.y >> 16) | (v1.y & 0xffff0000u);
-      dst[4 * row32] = (v0.z & 0xffffu) | (v1.z << 16);
-      dst[5 * row32] = (v0.z >> 16) | (v1.z & 0xffff0000u);
-      dst[6 * row32] = (v0.w & 0xffffu) | (v1.w << 16);
-      dst[7 * row32] = (v0.w >> 16) | (v1.w & 0xffff0000u);
-    }
-  };
-
-  if (ks0 < ks1) {
-    load_tile(ks0);
-    store_tile();
-  }
-  __syncthreads();
-  for (int kb = ks0; kb < ks1; kb += kBN) {
-    const bool has_next = kb + kBN < ks1;
-    if (has_next) load_tile(kb + kBN);  // in flight while this tile is computed
-
-    const int kw = kb + khalf * KEYS_PER_WAVE;  // first key of this wave's share
-    if (wave_active && kw <= wave_kmax && kw < ks1) {
-      f32x16 s[NKT];
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
-#pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) {
-          const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(
-              &Ks[(khalf * KEYS_PER_WAVE + kt * 32 + col) * KP + ds * 16 + half * 8]));
-          s[kt] = mfma32(ka, qf[ds], s[kt]);
-        }
+      for (int ds = 0; ds < NDS; ++ds) {
+        const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
+        s[kt] = mfma32(ka, qf[ds], s[kt]);
       }
-      // Mask keys past this column's causal limit or past the split.
-      const bool need_mask = (kw + KEYS_PER_WAVE - 1 > wave_kmin) || (kw + KEYS_PER_WAVE > ks1);
-      float mx = -INFINITY;
+    }
+    // Mask keys past this column's causal limit or past the split.
+    if (kw + KPW - 1 > wave_kmin || kw + KPW > ks1) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          if (need_mask) {
-            const int key = kw + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
-            if (key > lim || key >= ks1) s[kt][r] = -INFINITY;
-          }
-          mx = fmaxf(mx, s[kt][r]);
+          const int key = kw + kt * 32 + 8 * (r / 4) + 4 * half + (r % 4);
+          s[kt][r] = key > lim ? -INFINITY : s[kt][r];
         }
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_new = fmaxf(m_run, mx * c);
-      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
-      const float alpha = fast_exp2(m_run - m_use);
-      float psum = 0.0f;
-      bf16x8 pb[NKT][2];
+    }
+    float mx = -INFINITY;
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          float pv[8];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) pv[e] = fast_exp2(fmaf(s[kt][hh * 8 + e], c, -m_use));
-          u32x4 w;
-          w.x = pack_bf16x2(pv[0], pv[1]);
-          w.y = pack_bf16x2(pv[2], pv[3]);
-          w.z = pack_bf16x2(pv[4], pv[5]);
-          w.w = pack_bf16x2(pv[6], pv[7]);
-          // The normaliser sums the bf16 weights the PV product actually uses,
-          // so the output stays an exact convex combination of the values.
-          psum += (bf16_lo(w.x) + bf16_hi(w.x)) + (bf16_lo(w.y) + bf16_hi(w.y)) +
-                  (bf16_lo(w.z) + bf16_hi(w.z)) + (bf16_lo(w.w) + bf16_hi(w.w));
-          pb[kt][hh] = as_bf16x8(w);
-        }
-      l_run = l_run * alpha + psum;
-      m_run = m_new;
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+    const float mt = pair_max32(mx) * c;  // tile max of the column, log2 units
+    if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mt);
+      const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
+      l_run *= alpha;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[t][r] *= alpha;
-      // O^T += V^T P^T.  Lane half `half` supplies k-slots holding keys
-      // kw + 32kt + 16hh + 4half + {0..3} and + 8 + {0..3} (the S^T C rows it owns).
-#pragma unroll
-      for (int t = 0; t < NDT; ++t)
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const uint16_t *vp = &Vt[(t * 32 + col) * VP + khalf * KEYS_PER_WAVE + kt * 32 + hh * 16 + half * 4];
-            const u32x2 lo = *reinterpret_cast<const u32x2 *>(vp);
-            const u32x2 hi = *reinterpret_cast<const u32x2 *>(vp + 8);
-            acc[t] = mfma32(as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y}), pb[kt][hh], acc[t]);
-          }
+      m_run = m_new;
     }
-    __syncthreads();  // every wave is done with this tile
-    if (has_next) {
-      store_tile();
-      __syncthreads();
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    bf16x8 pb[NKT][2];
+#pragma unroll
+    for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          typedef float f32x2 __attribute__((ext_vector_type(2)));
+          const f32x2 pv = {fast_exp2(fmaf(s[kt][hh * 8 + 2 * e], c, -m_use)),
+                            fast_exp2(fmaf(s[kt][hh * 8 + 2 * e + 1], c, -m_use))};
+          const bf16x2 pk = __builtin_convertvector(pv, bf16x2);
+          // The normaliser sums the bf16 weights the PV product uses, so the
+          // output stays an exact convex combination of the values.
+          l_run = __builtin_amdgcn_fdot2_f32_bf16(pk, ones, l_run, false);
+          w[e] = __builtin_bit_cast(uint32_t, pk);
+        }
+        pb[kt][hh] = as_bf16x8(w);
+      }
+    // O^T += V^T P^T.  B element e of k-step (kt, hh) is S^T register hh*8+e:
+    // key 32kt + 16hh + 8(e/4) + 4half + e%4, i.e. two runs of 4 keys, which the
+    // two transposing reads of each A operand supply.
+#pragma unroll
+    for (int t = 0; t < NDT; ++t)
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const uint16_t *vp = Vt + v_off[t] + (kt * 32 + hh * 16) * DP;
+          const u32x2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * DP);
+          acc[t] = mfma32(as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y}), pb[kt][hh], acc[t]);
+        }
+  };
+
+  // Pipeline: before computing tile t, wait for its loads (at most the loads of
+  // tiles t+1 .. t+NST-2 may stay outstanding), barrier (the tile is complete
+  // in LDS and every wave has finished tile t-1), then refill the stage of
+  // tile t-1 with tile t+NST-1.
+  // The query tile is read into registers at tile 0, after which a second
+  // barrier frees its buffer for tile NST-1.
+  constexpr int PER_TILE = 2 * LOADS;  // load instructions per tile per thread
+  if (ntile > 0) {
+    issue_query();
+#pragma unroll
+    for (int st = 0; st < NST - 1; ++st)
+      if (st < ntile) issue(st, ks0 + st * kBN);
+  }
+  for (int t0 = 0; t0 < ntile; t0 += NST) {
+#pragma unroll
+    for (int st = 0; st < NST; ++st) {
+      const int t = t0 + st;
+      if (t < ntile) {
+        const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
+        if constexpr (NST == 3) {
+          if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
+          else wait_loads_and_barrier<0>();
+        } else {
+          wait_loads_and_barrier<0>();
+        }
+        if (t == 0) {
+          const uint16_t *Qt = smem + (NST - 1) * 2 * TILE;
+#pragma unroll
+          for (int ds = 0; ds < NDS; ++ds)
+            qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
+                Qt + jr0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+          wait_lds_and_barrier();
+        }
+        if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * kBN);
+        compute(st, ks0 + t * kBN);
+      }
     }
   }
 
   // Per-lane partial sum -> column sum (lanes l and l^32 hold the two key halves of a 32x32 tile).
-  l_run += __shfl_xor(l_run, 32);
+  l_run = pair_sum32(l_run);
   if constexpr (KH > 1) {
-    // Fold the second key half (waves 4..7) into waves 0..3.
+    // Fold the second key slice (waves 4..7) into waves 0..3, through LDS.
+    float(*xchg)[NDT * 16 + 2][64] = reinterpret_cast<float(*)[NDT * 16 + 2][64]>(smem);
+    wait_loads_and_barrier<0>();  // every wave is done with the tiles
     if (khalf == 1) {
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
@@ -332,11 +454,14 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   }
 }
 
+// Blocks per launch: the item count rounded up to a multiple of the 8 XCDs
+// (blocks past the last item exit at once).
 hipError_t launch_prefill(const AttnArgs &a, int dp, int items, hipStream_t stream) {
+  const dim3 grid((items + 7) / 8 * 8);
   switch (dp) {
-    case 64: hipLaunchKernelGGL((prefill_kernel<64, 1>), dim3(items), dim3(256), 0, stream, a); break;
-    case 128: hipLaunchKernelGGL((prefill_kernel<128, 2>), dim3(items), dim3(512), 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<256, 1>), dim3(items), dim3(256), 0, stream, a); break;
+    case 64: hipLaunchKernelGGL((prefill_kernel<64, 2>), grid, dim3(512), 0, stream, a); break;
+    case 128: hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, dim3(512), 0, stream, a); break;
+    default: hipLaunchKernelGGL((prefill_kernel<256, 1>), grid, dim3(256), 0, stream, a); break;
   }
   return hipGetLastError();
 }

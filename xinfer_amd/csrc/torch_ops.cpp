@@ -45,6 +45,11 @@ bool kernel_layout(const at::Tensor &t) {
   return true;
 }
 
+// Q additionally fits one batch row ([Hq, T, D]) in 32-bit byte offsets.
+bool query_layout(const at::Tensor &q) {
+  return kernel_layout(q) && (q.size(1) * q.stride(1) + q.size(2) * q.stride(2)) * 2 < (int64_t(1) << 31);
+}
+
 void *current_stream(const at::Tensor &t) {
   return static_cast<void *>(c10::hip::getCurrentHIPStream(t.device().index()).stream());
 }
@@ -91,7 +96,7 @@ at::Tensor batched_flash_attention(const at::Tensor &q, const at::Tensor &k, con
   // batched_attention_metadata and needs no read.  Copy only what the kernels
   // cannot read in place, as the reference does (:58-61, :108-114); a copy of
   // the longest populated prefix covers every key any row reads.
-  auto query = kernel_layout(q) ? q : q.contiguous();
+  auto query = query_layout(q) ? q : q.contiguous();
   auto key = kernel_layout(k) ? k : k.narrow(2, 0, max_length).contiguous();
   auto value = kernel_layout(v) ? v : v.narrow(2, 0, max_length).contiguous();
   if (key.size(2) != value.size(2)) {
@@ -131,7 +136,7 @@ at::Tensor flash_attention(const at::Tensor &q, const at::Tensor &k, const at::T
   TORCH_CHECK(!q.requires_grad() && !k.requires_grad() && !v.requires_grad(),
               "xinfer attention supports inference only");
   c10::DeviceGuard guard(q.device());
-  auto query = kernel_layout(q) ? q : q.contiguous();
+  auto query = query_layout(q) ? q : q.contiguous();
   auto key = kernel_layout(k) ? k : k.slice(2, 0, length).contiguous();
   auto value = kernel_layout(v) ? v : v.slice(2, 0, length).contiguous();
   if (key.size(2) != value.size(2)) {
