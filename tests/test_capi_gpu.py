@@ -111,3 +111,66 @@ def test_flash_and_append_through_c_abi(capi, gpu_ops):
 
     via_torch = gpu_ops.flash_attention(q, k, v, cache_extent(length), dim**-0.5)
     assert torch.equal(out.view(torch.int16), via_torch.view(torch.int16))
+
+
+@torch.inference_mode()
+def test_split_merge_survives_garbage_and_reused_workspace(capi, gpu_ops):
+    """Split rows merge inside the attention launch through arrival counters in
+    the workspace.  A workspace full of arbitrary bytes, then the same workspace
+    reused by later calls on other inputs, must still give the torch results."""
+    torch.manual_seed(79)
+    batch, heads, kv_heads, dim, capacity = 3, 16, 8, 128, 16384
+    counts, lengths = [1, 200, 1], [13000, 5000, 3000]
+    log(f"C ABI split merge counts={counts} lengths={lengths}")
+    host, cu, blocks = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
+    offsets = host.contiguous()
+    host_ptr = ctypes.cast(offsets.data_ptr(), ctypes.POINTER(ctypes.c_int32))
+    k = torch.randn(batch, kv_heads, capacity, dim, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    q0 = torch.randn(batch, heads, max(counts), dim, device="cuda", dtype=torch.bfloat16)
+    size = capi.xinfer_batched_flash_attention_workspace_size(
+        ctypes.byref(view(q0)), ctypes.byref(view(k)), host_ptr)
+    assert size > 0
+    for fill in ("ones", "random", "reuse", "reuse"):
+        q = torch.randn_like(q0)
+        if fill == "ones":
+            workspace = torch.full((size,), 0xFF, dtype=torch.uint8, device="cuda")
+        elif fill == "random":
+            workspace = torch.randint(0, 256, (size,), dtype=torch.uint8, device="cuda")
+        out = torch.empty_like(q)
+        status = capi.xinfer_batched_flash_attention(
+            ctypes.byref(view(q)), ctypes.byref(view(k)), ctypes.byref(view(v)), host_ptr,
+            ctypes.c_double(dim**-0.5), ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()),
+            ctypes.c_size_t(size), stream())
+        assert status == 0, capi.xinfer_status_string(status)
+        via_torch = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)
+        assert torch.equal(out.view(torch.int16), via_torch.view(torch.int16)), fill
+
+
+@torch.inference_mode()
+def test_split_merge_in_graph_replays(gpu_ops):
+    """A captured call replays with the same arrival counters: every replay,
+    on new inputs copied into the captured buffers, matches an eager call."""
+    torch.manual_seed(80)
+    batch, heads, kv_heads, dim, capacity = 2, 16, 8, 128, 8192
+    counts, lengths = [1, 512], [8000, 2048]
+    log(f"graph replay split merge counts={counts} lengths={lengths}")
+    host, cu, blocks = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
+    q = torch.randn(batch, heads, max(counts), dim, device="cuda", dtype=torch.bfloat16)
+    k = torch.randn(batch, kv_heads, capacity, dim, device="cuda", dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)  # warm-up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)
+    for replay in range(4):
+        q.copy_(torch.randn_like(q))
+        k[:, :, :64].copy_(torch.randn_like(k[:, :, :64]))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)
+        torch.cuda.synchronize()
+        assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), replay

@@ -129,13 +129,16 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
         grp.pre_items += (int)(g.Hkv * rs.ntiles * rs.nsplit);
       }
       if (rs.nsplit > 1) {
+        // Decode: [kv head][split][vector] records.  Prefill: per (kv head,
+        // split, query tile) a block of kPrefillTileQ records.
         rs.rec_begin = plan.records;
-        plan.records += g.Hkv * rs.nsplit * qv;
+        plan.records += g.Hkv * rs.nsplit * (decode ? qv : rs.ntiles * kPrefillTileQ);
         MergeRow &mr = grp.merge.rows[grp.merge.nrows++];
         mr.batch = (int32_t)b;
         mr.count = cnt;
         mr.nsplit = rs.nsplit;
         mr.item_begin = grp.merge_items;
+        mr.tiles = decode ? 0 : rs.ntiles;
         mr.rec_begin = rs.rec_begin;
         grp.merge_items += (int)(g.Hkv * qv);
         grp.merge_max_splits = std::max(grp.merge_max_splits, (int)rs.nsplit);

@@ -46,6 +46,9 @@ struct MergeRow {
   int32_t count;       // real queries of the row
   int32_t nsplit;      // records per query vector (> 1)
   int32_t item_begin;  // first merge work item (blockIdx.x) of this row
+  int32_t tiles;       // 0: [kv head][split][vector] records (decode); else the
+                       // prefill layout: per (kv head, split, query tile of 128
+                       // vectors) a block [D/4][128][4], `tiles` tiles per head
   int64_t rec_begin;   // first partial record of the row
 };
 

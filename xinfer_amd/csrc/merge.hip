@@ -17,10 +17,18 @@
 // SG = 1, one thread owning a vector's 4 features across all splits; with many
 // splits (long decode rows) one 256-thread block per vector spreads them over
 // SG = 256 / FC split lanes.
+//
+// Blocks are dealt to the 8 XCDs in contiguous runs of vectors (block b runs
+// vector group (b % 8) * (grid / 8) + b / 8), the order the prefill kernel
+// gives its items, so the records a head's tiles wrote through one XCD's L2
+// are mostly read back on that XCD.
 #include "device_common.h"
 #include "kernel_args.h"
 
 namespace xattn {
+
+// Query vectors per prefill record block (the prefill kernel's query tile).
+constexpr int kMergeTile = 128;
 
 struct MergeState {
   float m, l;
@@ -45,15 +53,36 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   constexpr int VPB = THREADS / (FC * SG);  // query vectors per block
   __shared__ MergeState red[SG > 1 ? SG : 1][SG > 1 ? FC : 1];
 
-  const int tid = threadIdx.x, f = tid % FC, sg = (tid / FC) % SG, vl = tid / (FC * SG);
-  const int vec = blockIdx.x * VPB + vl;
+  // Few splits: vectors vary fastest across a block's threads (the prefill
+  // record layout keeps a tile's vectors contiguous per feature group).
+  // Many splits: feature lanes vary fastest.
+  const int tid = threadIdx.x;
+  const int f = SG > 1 ? tid % FC : tid / VPB, sg = SG > 1 ? (tid / FC) % SG : 0;
+  const int vl = SG > 1 ? tid / (FC * SG) : tid % VPB;
+  const int group = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  const int vec = group * VPB + vl;
   const bool vvalid = vec < a.total_items;
   const MergeRow mr = a.rows[find_row(a.rows, a.nrows, vvalid ? vec : 0)];
   const int local = vec - mr.item_begin;
   const int qrows = mr.count * a.G;
   const int h = local / qrows, j = local - h * qrows;
-  const int64_t rec0 = mr.rec_begin + (int64_t)h * mr.nsplit * qrows + j;
   const int d = f * 4;
+  // Record s of this vector: o at part_o + o_base + s * o_step, (m, l) at
+  // part_ml + 2 * (ml_base + s * ml_step).
+  int64_t o_base, o_step, ml_base, ml_step;
+  if (mr.tiles == 0) {
+    ml_base = mr.rec_begin + (int64_t)h * mr.nsplit * qrows + j;
+    ml_step = qrows;
+    o_base = ml_base * a.D + d;
+    o_step = ml_step * a.D;
+  } else {
+    const int tile = j / kMergeTile, jr = j - tile * kMergeTile;
+    const int64_t blk = mr.rec_begin + ((int64_t)h * mr.nsplit * mr.tiles + tile) * kMergeTile;
+    ml_base = blk + jr;
+    ml_step = (int64_t)mr.tiles * kMergeTile;
+    o_base = blk * a.D + (f * kMergeTile + jr) * 4;
+    o_step = ml_step * a.D;
+  }
 
   MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
   if (vvalid && d < a.D) {
@@ -63,17 +92,17 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
       f32x4 o[4];
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int64_t rec = rec0 + (int64_t)(s + u * SG) * qrows;
-        ml[u] = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * rec);
-        o[u] = *reinterpret_cast<const f32x4 *>(a.part_o + rec * a.D + d);
+        const int64_t sp = s + u * SG;
+        ml[u] = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * (ml_base + sp * ml_step));
+        o[u] = *reinterpret_cast<const f32x4 *>(a.part_o + o_base + sp * o_step);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
     }
     for (; s < mr.nsplit; s += SG) {
-      const int64_t rec = rec0 + (int64_t)s * qrows;
-      const u32x2 ml = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * rec);
-      fold(st, __uint_as_float(ml.x), __uint_as_float(ml.y), *reinterpret_cast<const f32x4 *>(a.part_o + rec * a.D + d));
+      const u32x2 ml = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * (ml_base + (int64_t)s * ml_step));
+      fold(st, __uint_as_float(ml.x), __uint_as_float(ml.y),
+           *reinterpret_cast<const f32x4 *>(a.part_o + o_base + (int64_t)s * o_step));
     }
   }
   if constexpr (SG > 1) {
@@ -99,11 +128,13 @@ constexpr int kMergeSerialSplits = 8;
 template <int DP>
 static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t stream) {
   constexpr int FC = DP / 4;
+  // Grids are rounded up to a multiple of the 8 XCDs; surplus vectors exit.
   if (max_splits <= kMergeSerialSplits) {
     constexpr int VPB = 256 / FC;
-    hipLaunchKernelGGL((merge_kernel<DP, 1, 256>), dim3((a.total_items + VPB - 1) / VPB), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((merge_kernel<DP, 1, 256>), dim3(((a.total_items + VPB - 1) / VPB + 7) / 8 * 8), dim3(256), 0,
+                       stream, a);
   } else {
-    hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), dim3(a.total_items), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), dim3((a.total_items + 7) / 8 * 8), dim3(256), 0, stream, a);
   }
   return hipGetLastError();
 }

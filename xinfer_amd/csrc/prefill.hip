@@ -43,7 +43,8 @@
 // the accumulator rescale.  Weights exp2(s - m) then stay below 2^kRescaleSlack;
 // O and the normaliser use the same m, so the quotient is unchanged.
 //
-// Several splits of a tile write fp32 partial records, combined by merge.hip.
+// Several splits of a tile write fp32 partial records, combined by merge.hip;
+// a tile's records per split are laid out [D/4][128 vectors][4 features].
 // The tile-0 / split-0 item zeroes the row's padded queries (t >= count).
 #include "device_common.h"
 #include "kernel_args.h"
@@ -435,21 +436,21 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
                       pack_bf16x2(acc[t][r4 * 4 + 2] * inv, acc[t][r4 * 4 + 3] * inv)};
         }
     } else {
-      const int64_t rec = rs.rec_begin + ((int64_t)h * rs.nsplit + split) * qrows + j;
-      float *po = a.part_o + rec * D;
+      // Record block of (head, split, tile): [D/4][kTileQ][4] floats, so a
+      // store instruction writes two 512-byte runs of whole cache lines.
+      const int jr = j - tile * kTileQ;
+      const int64_t blk = rs.rec_begin + (((int64_t)h * rs.nsplit + split) * rs.ntiles + tile) * kTileQ;
+      float *po = a.part_o + blk * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
 #pragma unroll
         for (int r4 = 0; r4 < 4; ++r4) {
-          const int d = t * 32 + 8 * r4 + 4 * half;
-          if (d < D)
-            *reinterpret_cast<f32x4 *>(po + d) =
+          const int d4 = 8 * t + 2 * r4 + half;  // features 4*d4 .. 4*d4+3
+          if (d4 * 4 < D)
+            *reinterpret_cast<f32x4 *>(po + (d4 * kTileQ + jr) * 4) =
                 f32x4{acc[t][r4 * 4 + 0], acc[t][r4 * 4 + 1], acc[t][r4 * 4 + 2], acc[t][r4 * 4 + 3]};
         }
-      if (half == 0) {
-        a.part_ml[2 * rec] = m_run;
-        a.part_ml[2 * rec + 1] = l_run;
-      }
+      if (half == 0) *reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)) = u32x2{__float_as_uint(m_run), __float_as_uint(l_run)};
     }
   }
 }
