@@ -84,25 +84,23 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
     o_step = ml_step * a.D;
   }
 
+  // Every record of a batch is loaded before any is folded: a lane's splits
+  // take ceil(nsplit / (SG * INFLIGHT)) memory round trips.
+  constexpr int INFLIGHT = SG > 1 ? 16 : 4;
   MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
   if (vvalid && d < a.D) {
-    int s = sg;
-    for (; s + 3 * SG < mr.nsplit; s += 4 * SG) {  // four records in flight
-      u32x2 ml[4];
-      f32x4 o[4];
+    for (int s0 = sg; s0 < mr.nsplit; s0 += INFLIGHT * SG) {
+      u32x2 ml[INFLIGHT];
+      f32x4 o[INFLIGHT];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t sp = s + u * SG;
+      for (int u = 0; u < INFLIGHT; ++u) {
+        const int64_t sp = min(s0 + u * SG, mr.nsplit - 1);
         ml[u] = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * (ml_base + sp * ml_step));
         o[u] = *reinterpret_cast<const f32x4 *>(a.part_o + o_base + sp * o_step);
       }
 #pragma unroll
-      for (int u = 0; u < 4; ++u) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
-    }
-    for (; s < mr.nsplit; s += SG) {
-      const u32x2 ml = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * (ml_base + (int64_t)s * ml_step));
-      fold(st, __uint_as_float(ml.x), __uint_as_float(ml.y),
-           *reinterpret_cast<const f32x4 *>(a.part_o + o_base + (int64_t)s * o_step));
+      for (int u = 0; u < INFLIGHT; ++u)
+        if (s0 + u * SG < mr.nsplit) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
     }
   }
   if constexpr (SG > 1) {
