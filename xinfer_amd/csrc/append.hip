@@ -23,21 +23,36 @@ __global__ void __launch_bounds__(256) append_kv_kernel(const AppendArgs a) {
   const int64_t unit = (int64_t)blockIdx.x * 256 + threadIdx.x;
   const int token = (int)(unit / per_token), part = (int)(unit % per_token);
   if (token >= a.T) return;
+  // The new key/value rows are loaded together with the row's count (they lie
+  // inside the [B, H, T, D] inputs for every token < T); the position is read
+  // only for real tokens, so the copy takes two dependent memory round trips.
+  const uint16_t *key = a.key.p + row * a.key.sb + head * a.key.sh + token * a.key.st;
+  const uint16_t *value = a.value.p + row * a.value.sb + head * a.value.sh + token * a.value.st;
+  u32x4 kv[2];
+  uint16_t ks = 0, vs = 0;
+  if constexpr (kVector) {
+    kv[0] = load16(key + part * 8);
+    kv[1] = load16(value + part * 8);
+  } else {
+    ks = key[part * a.key_sd];
+    vs = value[part * a.value_sd];
+  }
   int count = a.cu_query[row + 1] - a.cu_query[row];
   count = count < 0 ? 0 : (count > a.T ? a.T : count);
+  // Keeps the key/value loads ahead of the branches below (the compiler would
+  // otherwise sink them after the position load).
+  if constexpr (kVector) asm volatile("" ::"v"(kv[0]), "v"(kv[1]));
+  else asm volatile("" ::"v"(ks), "v"(vs));
   if (token >= count) return;  // padded token: its position is never loaded
   const int64_t pos = a.positions[row * a.pos_sb + token * a.pos_st];
   if (pos < 0 || pos >= a.C) return;
   const int64_t dst = (((int64_t)row * a.H + head) * a.C + pos) * a.D;
-  const uint16_t *key = a.key.p + row * a.key.sb + head * a.key.sh + token * a.key.st;
-  const uint16_t *value = a.value.p + row * a.value.sb + head * a.value.sh + token * a.value.st;
   if constexpr (kVector) {
-    const int f = part * 8;
-    store16(a.cache_key + dst + f, load16(key + f));
-    store16(a.cache_value + dst + f, load16(value + f));
+    store16(a.cache_key + dst + part * 8, kv[0]);
+    store16(a.cache_value + dst + part * 8, kv[1]);
   } else {
-    a.cache_key[dst + part] = key[part * a.key_sd];
-    a.cache_value[dst + part] = value[part * a.value_sd];
+    a.cache_key[dst + part] = ks;
+    a.cache_value[dst + part] = vs;
   }
 }
 
