@@ -10,7 +10,7 @@
 // Work item = (row, kv head, chunk of TOK_ITEM keys); the chunk's K and V are
 // read from HBM exactly once and shared by the G grouped query heads.  One
 // block per item; every K/V load of the block (8 rows of 16 bytes per lane and
-// tensor for 2 query vectors) is issued before any arithmetic, and the small
+// tensor, 4 for 8 query vectors) is issued before any arithmetic, and the small
 // register footprint keeps several blocks resident per CU, so the loads of
 // some blocks are in flight while others compute (measured on MI355X: 32 KB
 // per tensor per block is the read shape that sustains the most bandwidth).
@@ -45,7 +45,9 @@ struct DecodeShape {
   static constexpr int LPT = DP / 8;             // lanes per key row
   static constexpr int TPW = 64 / LPT;           // key rows per wave instruction
   static constexpr int U = QR <= 2 ? 4 : (QR == 4 ? 2 : 1);  // rows per lane per block
-  static constexpr int NB = 2;                   // blocks per wave per item
+  // Blocks per wave per item: 16 KB of K+V per wave (8 KB for 8 query
+  // vectors, whose accumulators take the registers).
+  static constexpr int NB = QR == 8 ? 4 : 8 / U;
   static constexpr int BLK = TPW * U;            // keys per wave block
   static constexpr int TOK_WAVE = NB * BLK;      // keys per wave per item
   static constexpr int TOK_ITEM = 4 * TOK_WAVE;  // keys per work item
@@ -271,7 +273,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
 
 int decode_tokens_per_item(int dp, int qr) {
   const int u = qr <= 2 ? 4 : (qr == 4 ? 2 : 1);
-  return 4 * 2 * (64 / (dp / 8)) * u;
+  return 4 * (qr == 8 ? 4 : 8 / u) * (64 / (dp / 8)) * u;
 }
 
 template <int DP>

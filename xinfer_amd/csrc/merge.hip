@@ -15,8 +15,9 @@
 // A block is VPB query vectors x SG split lanes x FC feature lanes (4
 // features each): with few splits per vector (prefill) a 256-thread block has
 // SG = 1, one thread owning a vector's 4 features across all splits; with many
-// splits (long decode rows) one 256-thread block per vector spreads them over
-// SG = 256 / FC split lanes.
+// splits (long decode rows) one block per vector spreads them over SG =
+// THREADS / FC split lanes, THREADS (256, 512 or 1024) chosen so that a lane
+// loads at most one batch of 16 records.
 //
 // Blocks are dealt to the 8 XCDs in contiguous runs of vectors (block b runs
 // vector group (b % 8) * (grid / 8) + b / 8), the order the prefill kernel
@@ -132,7 +133,15 @@ static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t
     hipLaunchKernelGGL((merge_kernel<DP, 1, 256>), dim3(((a.total_items + VPB - 1) / VPB + 7) / 8 * 8), dim3(256), 0,
                        stream, a);
   } else {
-    hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), dim3((a.total_items + 7) / 8 * 8), dim3(256), 0, stream, a);
+    // One block per vector, with enough split lanes that each lane loads at
+    // most one batch of 16 records when the block can grow to 1024 threads.
+    const dim3 grid((a.total_items + 7) / 8 * 8);
+    if (max_splits <= 16 * (256 / FC))
+      hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), grid, dim3(256), 0, stream, a);
+    else if (max_splits <= 16 * (512 / FC))
+      hipLaunchKernelGGL((merge_kernel<DP, 512 / FC, 512>), grid, dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL((merge_kernel<DP, 1024 / FC, 1024>), grid, dim3(1024), 0, stream, a);
   }
   return hipGetLastError();
 }
