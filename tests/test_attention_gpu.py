@@ -172,6 +172,23 @@ def test_long_prefix_and_tensor_derived_capacity(gpu_ops):
 
 
 @torch.inference_mode()
+def test_long_decode_rows_through_every_merge_layout(gpu_ops):
+    """Single-query rows long enough that the split merge takes each of its
+    block shapes (256, 512 and 1024 threads per query vector, and more than one
+    batch of records per lane), for head dims 128 and 256."""
+    op = gpu_ops.flash_attention.default
+    for heads, kv_heads, dim, lengths in ((8, 8, 128, (16384, 20000, 40000)), (16, 4, 256, (4000, 8000, 16384, 20000))):
+        capacity = max(lengths)
+        q, k, v = inputs(heads, kv_heads, dim, 1, capacity=capacity)
+        for length in lengths:
+            log(f"long decode row heads={heads}/{kv_heads} dim={dim} length={length}")
+            actual = op(q, k, v, cache_extent(length), dim**-0.5)
+            expected = reference_attention(q, k, v, [1], [length], dim**-0.5)
+            assert_close_rows(actual, expected, [1])
+            assert torch.equal(actual, op(q, k, v, cache_extent(length), dim**-0.5))
+
+
+@torch.inference_mode()
 def test_appended_chunks_use_lower_right_causality(gpu_ops):
     op = gpu_ops.flash_attention.default
     for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):
