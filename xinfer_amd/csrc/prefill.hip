@@ -129,7 +129,11 @@ struct PrefillShape {
   static constexpr int CHUNKS = DP / 8;               // 16-byte chunks per key row
   static constexpr int TILE = kBN * DP;               // bf16 elements of one K (or V) tile
   static constexpr int LOADS = kBN * CHUNKS / THREADS;  // 16-byte loads per thread per K (or V) tile
-  static constexpr int NST = 4 * TILE * 3 <= 100 * 1024 ? 3 : 2;  // tiles in flight (K+V: 4*TILE bytes)
+  // Tiles per barrier window (WIN) and LDS stages (K+V of a tile: 4*TILE
+  // bytes): two-tile windows over a ring of four stages when it fits in
+  // 128 KB, else one tile per barrier over a ring of 3 (or 2) stages.
+  static constexpr int WIN = 4 * TILE * 4 <= 128 * 1024 ? 2 : 1;
+  static constexpr int NST = WIN == 2 ? 4 : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2);
   static constexpr int KPW = kBN / KH;                // keys of each tile per wave
   static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
   static constexpr int FOLD = KH > 1 ? 4 * (NDT * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
@@ -352,41 +356,69 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
         }
   };
 
-  // Pipeline: before computing tile t, wait for its loads (at most the loads of
-  // tiles t+1 .. t+NST-2 may stay outstanding), barrier (the tile is complete
-  // in LDS and every wave has finished tile t-1), then refill the stage of
-  // tile t-1 with tile t+NST-1.
-  // The query tile is read into registers at tile 0, after which a second
-  // barrier frees its buffer for tile NST-1.
+  // Pipeline.  The query tile is read into registers at tile 0, after which
+  // a second barrier frees its buffer (the last stage).
   constexpr int PER_TILE = 2 * LOADS;  // load instructions per tile per thread
-  if (ntile > 0) {
-    issue_query();
+  auto read_query = [&]() {
+    const uint16_t *Qt = smem + (NST - 1) * 2 * TILE;
 #pragma unroll
-    for (int st = 0; st < NST - 1; ++st)
-      if (st < ntile) issue(st, ks0 + st * kBN);
-  }
-  for (int t0 = 0; t0 < ntile; t0 += NST) {
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[ds] = as_bf16x8(
+          *reinterpret_cast<const u32x4 *>(Qt + jr0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+    wait_lds_and_barrier();
+  };
+  if constexpr (S::WIN == 2) {
+    // Two-tile windows over four stages: at the start of the window of tiles
+    // t, t+1 wait for their loads and synchronise (every wave is done with
+    // tiles t-2 and t-1), refill those two stages with tiles t+2, t+3, then
+    // compute both tiles with no barrier between them, so the waves of a
+    // SIMD drift apart and overlap each other's MFMA, LDS and softmax phases.
+    if (ntile > 0) {
+      issue_query();
+      issue(0, ks0);
+      if (ntile > 1) issue(1, ks0 + kBN);
+    }
+    for (int t0 = 0; t0 < ntile; t0 += 4) {
 #pragma unroll
-    for (int st = 0; st < NST; ++st) {
-      const int t = t0 + st;
-      if (t < ntile) {
-        const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
-        if constexpr (NST == 3) {
-          if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
-          else wait_loads_and_barrier<0>();
-        } else {
+      for (int w = 0; w < 2; ++w) {
+        const int t = t0 + 2 * w;
+        if (t < ntile) {
           wait_loads_and_barrier<0>();
+          if (t == 0) read_query();
+          if (t + 2 < ntile) issue((2 * w + 2) % 4, ks0 + (t + 2) * kBN);
+          if (t + 3 < ntile) issue((2 * w + 3) % 4, ks0 + (t + 3) * kBN);
+          compute(2 * w, ks0 + t * kBN);
+          if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * kBN);
         }
-        if (t == 0) {
-          const uint16_t *Qt = smem + (NST - 1) * 2 * TILE;
+      }
+    }
+  } else {
+    // One tile per barrier: before computing tile t, wait for its loads (the
+    // loads of tiles t+1 .. t+NST-2 may stay outstanding), barrier (the tile
+    // is complete in LDS and every wave has finished tile t-1), then refill
+    // the stage of tile t-1 with tile t+NST-1.
+    if (ntile > 0) {
+      issue_query();
 #pragma unroll
-          for (int ds = 0; ds < NDS; ++ds)
-            qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(
-                Qt + jr0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
-          wait_lds_and_barrier();
+      for (int st = 0; st < NST - 1; ++st)
+        if (st < ntile) issue(st, ks0 + st * kBN);
+    }
+    for (int t0 = 0; t0 < ntile; t0 += NST) {
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const int t = t0 + st;
+        if (t < ntile) {
+          const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
+          if constexpr (NST == 3) {
+            if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
+            else wait_loads_and_barrier<0>();
+          } else {
+            wait_loads_and_barrier<0>();
+          }
+          if (t == 0) read_query();
+          if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * kBN);
+          compute(st, ks0 + t * kBN);
         }
-        if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * kBN);
-        compute(st, ks0 + t * kBN);
       }
     }
   }
