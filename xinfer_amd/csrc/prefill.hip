@@ -12,7 +12,8 @@
 // Waves: four query groups of 32 vectors x KH key slices.  With KH = 2 (head
 // dims 64 and 128) a block is 8 waves, two per SIMD, so one wave's MFMAs
 // overlap the other's softmax; wave w+4 takes keys 32..63 of every 64-key
-// tile and is folded into wave w at the end.  Each wave computes the
+// tile.  At the end waves w and w+4 exchange halves of their accumulators and
+// each finishes (and writes) half of the features.  Each wave computes the
 // transposed problem with v_mfma_f32_32x32x16_bf16:
 //   S^T[key, j]  = K[key, :] . Q[j, :]      A = K tile (LDS), B = Q^T (registers)
 //   O^T[d, j]   += V^T[d, key] P^T[key, j]  A = V^T (LDS, transposing reads), B = P^T
@@ -136,7 +137,8 @@ struct PrefillShape {
   static constexpr int NST = WIN == 2 ? 4 : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2);
   static constexpr int KPW = kBN / KH;                // keys of each tile per wave
   static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
-  static constexpr int FOLD = KH > 1 ? 4 * (NDT * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
+  static constexpr int HALF_T = KH > 1 ? NDT / 2 : NDT;  // d tiles each wave finishes
+  static constexpr int FOLD = KH > 1 ? 8 * (HALF_T * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
   static constexpr int SMEM = (NST * 4 * TILE > FOLD ? NST * 4 * TILE : FOLD);
 };
 
@@ -425,47 +427,56 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
 
   // Per-lane partial sum -> column sum (lanes l and l^32 hold the two key halves of a 32x32 tile).
   l_run = pair_sum32(l_run);
+  // Fold of the two key slices.  Waves w and w+4 hold the same 32 query
+  // vectors; wave w finishes d tiles 0 .. NDT/2-1 and wave w+4 the others:
+  // each hands the other's half of its accumulator, and its (m, l), through
+  // LDS, combines the half it keeps and writes that half of the output.
+  constexpr int HALF_T = S::HALF_T;
+  const int t_first = KH > 1 ? khalf * HALF_T : 0;  // first d tile this wave finishes
   if constexpr (KH > 1) {
-    // Fold the second key slice (waves 4..7) into waves 0..3, through LDS.
-    float(*xchg)[NDT * 16 + 2][64] = reinterpret_cast<float(*)[NDT * 16 + 2][64]>(smem);
+    float(*xchg)[HALF_T * 16 + 2][64] = reinterpret_cast<float(*)[HALF_T * 16 + 2][64]>(smem);
     wait_loads_and_barrier<0>();  // every wave is done with the tiles
-    if (khalf == 1) {
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+    for (int t = 0; t < NDT; ++t)
+      if ((t < HALF_T) == (khalf == 1)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) xchg[qgroup][t * 16 + r][lane] = acc[t][r];
-      xchg[qgroup][NDT * 16][lane] = m_run;
-      xchg[qgroup][NDT * 16 + 1][lane] = l_run;
-    }
+        for (int r = 0; r < 16; ++r) xchg[wave][(t % HALF_T) * 16 + r][lane] = acc[t][r];
+      }
+    xchg[wave][HALF_T * 16][lane] = m_run;
+    xchg[wave][HALF_T * 16 + 1][lane] = l_run;
     __syncthreads();
-    if (khalf == 0) {
-      const float m_b = xchg[qgroup][NDT * 16][lane], l_b = xchg[qgroup][NDT * 16 + 1][lane];
-      const float mx = fmaxf(m_run, m_b);
-      const float mu = mx == -INFINITY ? 0.0f : mx;
-      const float wa = fast_exp2(m_run - mu), wb = fast_exp2(m_b - mu);
+    const int partner = wave ^ 4;
+    const float m_b = xchg[partner][HALF_T * 16][lane], l_b = xchg[partner][HALF_T * 16 + 1][lane];
+    const float mx = fmaxf(m_run, m_b);
+    const float mu = mx == -INFINITY ? 0.0f : mx;
+    const float wa = fast_exp2(m_run - mu), wb = fast_exp2(m_b - mu);
 #pragma unroll
-      for (int t = 0; t < NDT; ++t)
+    for (int t = 0; t < NDT; ++t)
+      if ((t < HALF_T) == (khalf == 0)) {
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[t][r] = acc[t][r] * wa + xchg[qgroup][t * 16 + r][lane] * wb;
-      l_run = l_run * wa + l_b * wb;
-      m_run = mx;
-    }
+        for (int r = 0; r < 16; ++r) acc[t][r] = acc[t][r] * wa + xchg[partner][(t % HALF_T) * 16 + r][lane] * wb;
+      }
+    l_run = l_run * wa + l_b * wb;
+    m_run = mx;
   }
 
-  // Epilogue (waves 0..3).  acc[t][r] = O^T[d = 32t + 8(r/4) + 4half + r%4][column j].
-  if (khalf == 0 && jvalid) {
+  // Epilogue: d tiles t_first .. t_first + HALF_T - 1 of this wave.
+  // acc[t][r] = O^T[d = 32t + 8(r/4) + 4half + r%4][column j].
+  if (jvalid) {
     if (rs.nsplit == 1) {
       const float inv = 1.0f / l_run;
       uint16_t *dst = a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)qi * a.o_st;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
+        if (t >= t_first && t < t_first + HALF_T) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int d = t * 32 + 8 * r4 + 4 * half;
-          if (d < D)
-            *reinterpret_cast<u32x2 *>(dst + d) =
-                u32x2{pack_bf16x2(acc[t][r4 * 4 + 0] * inv, acc[t][r4 * 4 + 1] * inv),
-                      pack_bf16x2(acc[t][r4 * 4 + 2] * inv, acc[t][r4 * 4 + 3] * inv)};
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int d = t * 32 + 8 * r4 + 4 * half;
+            if (d < D)
+              *reinterpret_cast<u32x2 *>(dst + d) =
+                  u32x2{pack_bf16x2(acc[t][r4 * 4 + 0] * inv, acc[t][r4 * 4 + 1] * inv),
+                        pack_bf16x2(acc[t][r4 * 4 + 2] * inv, acc[t][r4 * 4 + 3] * inv)};
+          }
         }
     } else {
       // Record block of (head, split, tile): [D/4][kTileQ][4] floats, so a
@@ -475,14 +486,17 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       float *po = a.part_o + blk * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t)
+        if (t >= t_first && t < t_first + HALF_T) {
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          const int d4 = 8 * t + 2 * r4 + half;  // features 4*d4 .. 4*d4+3
-          if (d4 * 4 < D)
-            *reinterpret_cast<f32x4 *>(po + (d4 * kTileQ + jr) * 4) =
-                f32x4{acc[t][r4 * 4 + 0], acc[t][r4 * 4 + 1], acc[t][r4 * 4 + 2], acc[t][r4 * 4 + 3]};
+          for (int r4 = 0; r4 < 4; ++r4) {
+            const int d4 = 8 * t + 2 * r4 + half;  // features 4*d4 .. 4*d4+3
+            if (d4 * 4 < D)
+              *reinterpret_cast<f32x4 *>(po + (d4 * kTileQ + jr) * 4) =
+                  f32x4{acc[t][r4 * 4 + 0], acc[t][r4 * 4 + 1], acc[t][r4 * 4 + 2], acc[t][r4 * 4 + 3]};
+          }
         }
-      if (half == 0) *reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)) = u32x2{__float_as_uint(m_run), __float_as_uint(l_run)};
+      if (half == 0 && khalf == 0)
+        *reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)) = u32x2{__float_as_uint(m_run), __float_as_uint(l_run)};
     }
   }
 }
