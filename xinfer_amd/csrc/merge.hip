@@ -59,7 +59,9 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   // Many splits: feature lanes vary fastest.
   const int tid = threadIdx.x;
   const int f = SG > 1 ? tid % FC : tid / VPB, sg = SG > 1 ? (tid / FC) % SG : 0;
-  const int vl = SG > 1 ? tid / (FC * SG) : tid % VPB;
+  // With one vector per block the vector (and its row) is block-uniform, so
+  // the row lookup stays in scalar registers.
+  const int vl = VPB == 1 ? 0 : (SG > 1 ? tid / (FC * SG) : tid % VPB);
   const int group = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
   const int vec = group * VPB + vl;
   const bool vvalid = vec < a.total_items;
