@@ -40,12 +40,15 @@ AOTITorchError aoti_torch_cuda_batched_flash_attention(AtenTensorHandle q, AtenT
 
 /* New: the reference's append is a Triton op (compiler/common/kernels/kv_cache.py:45-72)
  * that AOTI compiles into the wrapper; the native op needs its own shim.  It
- * mutates cache_key/cache_value in place and returns no handle. */
+ * mutates cache_key/cache_value in place and returns nothing.  AOTInductor's
+ * wrapper passes one output slot for the operator's empty result, always
+ * null; it is never written. */
 AOTITorchError aoti_torch_cuda_append_kv_batched(AtenTensorHandle key, AtenTensorHandle value,
                                                  AtenTensorHandle positions,
                                                  AtenTensorHandle cu_query,
                                                  AtenTensorHandle cache_key,
-                                                 AtenTensorHandle cache_value);
+                                                 AtenTensorHandle cache_value,
+                                                 AtenTensorHandle *unused_output);
 
 #ifdef __cplusplus
 }

@@ -28,7 +28,8 @@ BATCHED_ATTENTION_C_SHIM = """AOTITorchError aoti_torch_cuda_batched_flash_atten
     double scale, AtenTensorHandle* output)"""
 APPEND_KV_C_SHIM = """AOTITorchError aoti_torch_cuda_append_kv_batched(
     AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle positions,
-    AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value)"""
+    AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value,
+    AtenTensorHandle* unused_output)"""
 MODELS = ("qwen3", "qwen35")
 _loaded = None
 

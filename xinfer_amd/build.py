@@ -98,10 +98,14 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     objects = [OBJ_DIR / f"{name}.o" for name in (*KERNEL_SOURCES, *HOST_SOURCES, *TORCH_SOURCES)]
     output = LIB_DIR / LIBRARY_NAME
     temporary = output.with_suffix(".so.tmp")
+    # -z nodelete: the operators are registered with the process-wide
+    # dispatcher, and Python keeps handles to them (torch.ops.xinfer.*), so the
+    # library stays mapped after the last dlclose, e.g. when the AOTInductor
+    # package that brought it in is dropped and another one is loaded later.
     _run(
         [compiler, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objects, "-o", temporary,
          f"-L{torch_lib}", "-ltorch", "-ltorch_cpu", "-ltorch_hip", "-lc10", "-lc10_hip", "-lamdhip64",
-         f"-Wl,-rpath,{torch_lib}", f"-Wl,-soname,{LIBRARY_NAME}", "-Wl,--no-undefined"],
+         f"-Wl,-rpath,{torch_lib}", f"-Wl,-soname,{LIBRARY_NAME}", "-Wl,--no-undefined", "-Wl,-z,nodelete"],
         verbose,
     )
     os.replace(temporary, output)

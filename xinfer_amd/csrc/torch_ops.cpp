@@ -230,7 +230,7 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_flash_attention(AtenTensorHandl
 
 AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_append_kv_batched(
     AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle positions, AtenTensorHandle cu_query,
-    AtenTensorHandle cache_key, AtenTensorHandle cache_value) {
+    AtenTensorHandle cache_key, AtenTensorHandle cache_value, AtenTensorHandle * /*unused_output*/) {
   AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
     xinfer::append_kv_batched(resolve_tensor_dispatch_flags(key), resolve_tensor_dispatch_flags(value),
                               resolve_tensor_dispatch_flags(positions),
