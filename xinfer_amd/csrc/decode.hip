@@ -58,8 +58,18 @@ struct DecodeItem {
   int64_t rec_begin;
 };
 
-__device__ __forceinline__ DecodeItem locate_item(const AttnArgs &a, int item, int tok_item) {
-  const RowSched rs = a.rows[find_row(a.rows, a.nrows, item)];
+// The arguments a decode block uses (named as in AttnArgs), pinned in SGPRs by
+// the kernel's prologue.
+struct DecodeParams {
+  View q, k, v;
+  uint16_t *out;
+  int64_t o_sb, o_sh, o_st;
+  float *part_o, *part_ml;
+  float scale_log2;
+  int32_t D, G, T;
+};
+
+__device__ __forceinline__ DecodeItem locate_item(const RowSched &rs, int item, int tok_item) {
   DecodeItem it;
   const int local = item - rs.item_begin;
   it.h = local / rs.nsplit;
@@ -82,7 +92,7 @@ struct DecodeRegs {
 };
 
 // Zero out[b, h*G + g, t, :] for g < G and t in [t_begin, T).
-__device__ __forceinline__ void zero_queries(const AttnArgs &a, int b, int h, int t_begin) {
+__device__ __forceinline__ void zero_queries(const DecodeParams &a, int b, int h, int t_begin) {
   const int per_head = (a.T - t_begin) * a.D / 8;  // 16-byte chunks per head
   for (int idx = threadIdx.x; idx < a.G * per_head; idx += blockDim.x) {
     const int g = idx / per_head, rest = idx - g * per_head;
@@ -93,7 +103,7 @@ __device__ __forceinline__ void zero_queries(const AttnArgs &a, int b, int h, in
 
 // Query features of the item's vectors (clamped into the row; zeroed past D later).
 template <int DP, int QR>
-__device__ __forceinline__ void load_query(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r, int dc) {
+__device__ __forceinline__ void load_query(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r, int dc) {
   const int qrows = it.cnt * a.G;
   const int dcc = dc * 8 < a.D ? dc : a.D / 8 - 1;
 #pragma unroll
@@ -107,7 +117,7 @@ __device__ __forceinline__ void load_query(const AttnArgs &a, const DecodeItem &
 // Issue every load of an item: K/V rows through buffer resources ending at the
 // item's last key, and the query features (clamped into the row, zeroed past D).
 template <int DP, int QR>
-__device__ __forceinline__ void issue_item(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
+__device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
                                            int wave, int slot, int dc) {
   using S = DecodeShape<DP, QR>;
   if (it.cnt == 0) return;
@@ -135,7 +145,7 @@ struct DecodeShared {
 
 // Compute one item from its registers; writes output or partial records.
 template <int DP, int QR>
-__device__ __forceinline__ void process_item(const AttnArgs &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
+__device__ __forceinline__ void process_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
                                              DecodeShared<DP, QR> &sh, int wave, int lane, int slot, int dc) {
   using S = DecodeShape<DP, QR>;
   constexpr int LPT = S::LPT, TPW = S::TPW, U = S::U, NB = S::NB, BLK = S::BLK;
@@ -265,10 +275,20 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   __shared__ DecodeShared<DP, QR> sh;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int slot = lane / S::LPT, dc = lane % S::LPT;
-  const DecodeItem it = locate_item(a, blockIdx.x, S::TOK_ITEM);
+  // Every argument of the block, loaded in one round trip (see XATTN_PIN_VIEW).
+  RowLookup<RowSched> rows;
+  rows.load(a.rows);
+  int nrows = a.nrows;
+  DecodeParams p{a.q, a.k, a.v, a.out, a.o_sb, a.o_sh, a.o_st, a.part_o, a.part_ml, a.scale_log2, a.D, a.G, a.T};
+  asm volatile(""
+               : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(nrows), XATTN_PIN_VIEW(p.q),
+                 XATTN_PIN_VIEW(p.k), XATTN_PIN_VIEW(p.v), "+s"(p.out), "+s"(p.o_sb), "+s"(p.o_sh), "+s"(p.o_st),
+                 "+s"(p.part_o), "+s"(p.part_ml), "+s"(p.scale_log2), "+s"(p.D), "+s"(p.G), "+s"(p.T));
+  const int item = blockIdx.x;
+  const DecodeItem it = locate_item(rows.find(a.rows, nrows, item), item, S::TOK_ITEM);
   DecodeRegs<DP, QR> r;
-  issue_item(a, it, r, wave, slot, dc);
-  process_item(a, it, r, sh, wave, lane, slot, dc);
+  issue_item(p, it, r, wave, slot, dc);
+  process_item(p, it, r, sh, wave, lane, slot, dc);
 }
 
 int decode_tokens_per_item(int dp, int qr) {

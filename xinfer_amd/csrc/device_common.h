@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "kernel_args.h"
+
 namespace xattn {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -130,13 +132,49 @@ __device__ __forceinline__ u32x4 buffer_load16_stream(__amdgpu_buffer_rsrc_t rsr
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 2));
 }
 
-// Locate the row owning work item `item`: rows are sorted by item_begin.
+// Kernel arguments reach a wave through scalar loads from the kernarg
+// segment.  The compiler issues each load next to its first use and may load a
+// value again at a later use, so a prologue that reads its arguments in stages
+// waits one memory round trip per stage.  A kernel therefore copies the
+// arguments it needs into locals and ties them all to SGPRs in ONE empty asm
+// statement (separate statements are scheduling boundaries, and the loads
+// would again come in stages): one round trip, and later uses read the
+// registers.  These macros spell the operand lists.
+#define XATTN_PIN_VIEW(v) "+s"((v).p), "+s"((v).sb), "+s"((v).sh), "+s"((v).st)
+#define XATTN_PIN_ROWSCHED(r)                                                                 \
+  "+s"((r).batch), "+s"((r).count), "+s"((r).length), "+s"((r).item_begin), "+s"((r).nsplit), \
+      "+s"((r).ntiles), "+s"((r).rec_begin)
+#define XATTN_PIN_MERGEROW(r)                                                                 \
+  "+s"((r).batch), "+s"((r).count), "+s"((r).nsplit), "+s"((r).item_begin), "+s"((r).tiles), \
+      "+s"((r).rec_begin)
+#define XATTN_PIN_BEGINS(l)                                                                   \
+  "+s"((l).begin[0]), "+s"((l).begin[1]), "+s"((l).begin[2]), "+s"((l).begin[3]),             \
+      "+s"((l).begin[4]), "+s"((l).begin[5]), "+s"((l).begin[6]), "+s"((l).begin[7])
+
+// Row lookup over a kernarg row table sorted by item_begin.  load() reads the
+// first eight item_begin values and row 0 (the tables always hold kMaxRows >= 8
+// rows, so the reads stay inside the arguments), to be pinned with the caller's
+// other arguments (XATTN_PIN_BEGINS and the row's list); find() then needs a
+// second round trip only for an item of a row other than 0, and a scan of the
+// table only past eight rows.
 template <typename Row>
-__device__ __forceinline__ int find_row(const Row *rows, int nrows, int item) {
-  int r = 0;
-  for (int k = 1; k < nrows; ++k)
-    if (rows[k].item_begin <= item) r = k;
-  return r;
-}
+struct RowLookup {
+  static_assert(kMaxRows >= 8, "row table");
+  int begin[8];
+  Row first;
+  __device__ __forceinline__ void load(const Row *rows) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) begin[k] = rows[k].item_begin;
+    first = rows[0];
+  }
+  __device__ __forceinline__ Row find(const Row *rows, int nrows, int item) const {
+    int r = 0;
+#pragma unroll
+    for (int k = 1; k < 8; ++k) r = (k < nrows && begin[k] <= item) ? k : r;
+    for (int k = 8; k < nrows; ++k)
+      if (rows[k].item_begin <= item) r = k;
+    return r == 0 ? first : rows[r];
+  }
+};
 
 }  // namespace xattn

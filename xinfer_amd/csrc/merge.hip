@@ -62,12 +62,24 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   // With one vector per block the vector (and its row) is block-uniform, so
   // the row lookup stays in scalar registers.
   const int vl = VPB == 1 ? 0 : (SG > 1 ? tid / (FC * SG) : tid % VPB);
-  const int group = (int)(blockIdx.x % 8) * (int)(gridDim.x / 8) + (int)(blockIdx.x / 8);
+  // Every argument of the block, loaded in one round trip (see XATTN_PIN_VIEW).
+  RowLookup<MergeRow> rows;
+  rows.load(a.rows);
+  int total_items = a.total_items, nrows = a.nrows, D = a.D, G = a.G;
+  uint16_t *out = a.out;
+  int64_t o_sb = a.o_sb, o_sh = a.o_sh, o_st = a.o_st;
+  const float *part_o = a.part_o, *part_ml = a.part_ml;
+  asm volatile(""
+               : XATTN_PIN_BEGINS(rows), XATTN_PIN_MERGEROW(rows.first), "+s"(total_items), "+s"(nrows), "+s"(D),
+                 "+s"(G), "+s"(out), "+s"(o_sb), "+s"(o_sh), "+s"(o_st), "+s"(part_o), "+s"(part_ml));
+  // The grid is the vector groups rounded up to a multiple of 8 (launch_merge_d).
+  const int groups = (total_items + VPB - 1) / VPB;
+  const int group = (int)(blockIdx.x % 8) * ((groups + 7) / 8) + (int)(blockIdx.x / 8);
   const int vec = group * VPB + vl;
-  const bool vvalid = vec < a.total_items;
-  const MergeRow mr = a.rows[find_row(a.rows, a.nrows, vvalid ? vec : 0)];
+  const bool vvalid = vec < total_items;
+  const MergeRow mr = rows.find(a.rows, nrows, vvalid ? vec : 0);
   const int local = vec - mr.item_begin;
-  const int qrows = mr.count * a.G;
+  const int qrows = mr.count * G;
   const int h = local / qrows, j = local - h * qrows;
   const int d = f * 4;
   // Record s of this vector: o at part_o + o_base + s * o_step, (m, l) at
@@ -76,30 +88,30 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   if (mr.tiles == 0) {
     ml_base = mr.rec_begin + (int64_t)h * mr.nsplit * qrows + j;
     ml_step = qrows;
-    o_base = ml_base * a.D + d;
-    o_step = ml_step * a.D;
+    o_base = ml_base * D + d;
+    o_step = ml_step * D;
   } else {
     const int tile = j / kMergeTile, jr = j - tile * kMergeTile;
     const int64_t blk = mr.rec_begin + ((int64_t)h * mr.nsplit * mr.tiles + tile) * kMergeTile;
     ml_base = blk + jr;
     ml_step = (int64_t)mr.tiles * kMergeTile;
-    o_base = blk * a.D + (f * kMergeTile + jr) * 4;
-    o_step = ml_step * a.D;
+    o_base = blk * D + (f * kMergeTile + jr) * 4;
+    o_step = ml_step * D;
   }
 
   // Every record of a batch is loaded before any is folded: a lane's splits
   // take ceil(nsplit / (SG * INFLIGHT)) memory round trips.
   constexpr int INFLIGHT = SG > 1 ? 16 : 4;
   MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
-  if (vvalid && d < a.D) {
+  if (vvalid && d < D) {
     for (int s0 = sg; s0 < mr.nsplit; s0 += INFLIGHT * SG) {
       u32x2 ml[INFLIGHT];
       f32x4 o[INFLIGHT];
 #pragma unroll
       for (int u = 0; u < INFLIGHT; ++u) {
         const int64_t sp = min(s0 + u * SG, mr.nsplit - 1);
-        ml[u] = *reinterpret_cast<const u32x2 *>(a.part_ml + 2 * (ml_base + sp * ml_step));
-        o[u] = *reinterpret_cast<const f32x4 *>(a.part_o + o_base + sp * o_step);
+        ml[u] = *reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step));
+        o[u] = *reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step);
       }
 #pragma unroll
       for (int u = 0; u < INFLIGHT; ++u)
@@ -115,10 +127,10 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
       fold(st, other.m, other.l, other.o);
     }
   }
-  if (!vvalid || d >= a.D) return;
+  if (!vvalid || d >= D) return;
   const float inv = 1.0f / st.l;
-  const int g = j % a.G, i = j / a.G;
-  uint16_t *dst = a.out + mr.batch * a.o_sb + (int64_t)(h * a.G + g) * a.o_sh + (int64_t)i * a.o_st;
+  const int g = j % G, i = j / G;
+  uint16_t *dst = out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st;
   *reinterpret_cast<u32x2 *>(dst + d) =
       u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
 }

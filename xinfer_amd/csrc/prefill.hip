@@ -164,24 +164,37 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int col = lane & 31, half = lane >> 5;
   const int qgroup = wave & 3, khalf = wave >> 2;
 
+  // The arguments the prologue needs, loaded in one round trip (see
+  // XATTN_PIN_VIEW).  The output pointers and strides are read in the
+  // epilogue instead: kept in SGPRs across the tile loop they cost more than
+  // the late load.
+  RowLookup<RowSched> rows;
+  rows.load(a.rows);
+  int total_items = a.total_items, nrows = a.nrows, G = a.G, D = a.D, T = a.T;
+  float c = a.scale_log2;
+  View qv = a.q, kv = a.k, vv = a.v;
+  asm volatile(""
+               : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(total_items), "+s"(nrows), "+s"(G),
+                 "+s"(D), "+s"(T), "+s"(c), XATTN_PIN_VIEW(qv), XATTN_PIN_VIEW(kv), XATTN_PIN_VIEW(vv));
   // The hardware hands consecutive blocks to the 8 XCDs in turn.  Block b runs
   // item (b % 8) * (grid / 8) + b / 8, so each XCD gets a contiguous run of
   // items; items are ordered (row, head, split, tile), so the tiles that read
   // the same keys share that XCD's L2.
-  const int nblocks = gridDim.x;
+  // The grid is total_items rounded up to a multiple of 8 (launch_prefill).
+  const int nblocks = (total_items + 7) / 8 * 8;
   const int item = (int)(blockIdx.x % 8) * (nblocks / 8) + (int)(blockIdx.x / 8);
-  if (item >= a.total_items) return;
-  const RowSched rs = a.rows[find_row(a.rows, a.nrows, item)];
+  if (item >= total_items) return;
+  const RowSched rs = rows.find(a.rows, nrows, item);
   const int local = item - rs.item_begin;
   const int per_head = rs.ntiles * rs.nsplit;
   const int h = local / per_head;
   const int split = (local - h * per_head) / rs.ntiles;
   const int tile = local - h * per_head - split * rs.ntiles;
-  const int b = rs.batch, L = rs.length, cnt = rs.count, G = a.G, D = a.D;
+  const int b = rs.batch, L = rs.length, cnt = rs.count;
   const int qrows = cnt * G, p0 = L - cnt;
 
-  if (tile == 0 && split == 0 && cnt < a.T) {  // zero the row's padded queries
-    const int per = (a.T - cnt) * D / 8;
+  if (tile == 0 && split == 0 && cnt < T) {  // zero the row's padded queries
+    const int per = (T - cnt) * D / 8;
     for (int idx = tid; idx < G * per; idx += THREADS) {
       const int g = idx / per, rest = idx - g * per;
       store16(a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)cnt * a.o_st + rest * 8,
@@ -212,9 +225,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // the tile: key q / CHUNKS, slot q % CHUNKS, holding chunk slot ^ swizzle.
   // Chunks past D (padded head dims) repeat the row's last chunk: finite
   // values that only meet zero query features or unused output rows.
-  const uint32_t k_row = (uint32_t)a.k.st * 2, v_row = (uint32_t)a.v.st * 2;
-  const u32x4 k_rsrc = buffer_words(a.k.p + b * a.k.sb + (int64_t)h * a.k.sh, (uint32_t)ks1 * k_row);
-  const u32x4 v_rsrc = buffer_words(a.v.p + b * a.v.sb + (int64_t)h * a.v.sh, (uint32_t)ks1 * v_row);
+  const uint32_t k_row = (uint32_t)kv.st * 2, v_row = (uint32_t)vv.st * 2;
+  const u32x4 k_rsrc = buffer_words(kv.p + b * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
+  const u32x4 v_rsrc = buffer_words(vv.p + b * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
   uint32_t k_voff[LOADS], v_voff[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
@@ -230,7 +243,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   constexpr int QLOADS = kTileQ * CHUNKS / THREADS;
   static_assert(kTileQ * CHUNKS == QLOADS * THREADS && kTileQ * DP <= 2 * TILE, "query tile fits a stage");
   auto issue_query = [&]() {
-    const u32x4 q_rsrc = buffer_words(a.q.p + b * a.q.sb + (int64_t)(h * G) * a.q.sh, 0x7fffffffu);
+    const u32x4 q_rsrc = buffer_words(qv.p + b * qv.sb + (int64_t)(h * G) * qv.sh, 0x7fffffffu);
     uint16_t *qdst = smem + (NST - 1) * 2 * TILE;
 #pragma unroll
     for (int i = 0; i < QLOADS; ++i) {
@@ -238,7 +251,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       const int jr = qs / CHUNKS, chunk = (qs % CHUNKS) ^ k_swizzle<CHUNKS>(jr);
       const int jq = tile * kTileQ + jr;
       const uint32_t off = (jq < qrows && chunk < D / 8)
-                               ? (uint32_t)(((jq % G) * a.q.sh + (jq / G) * a.q.st) * 2 + chunk * 16)
+                               ? (uint32_t)(((jq % G) * qv.sh + (jq / G) * qv.st) * 2 + chunk * 16)
                                : 0x80000000u;
       lds_load16(q_rsrc, lds_address(qdst + (wave * QLOADS + i) * 512), off, 0);
     }
@@ -278,7 +291,6 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) acc[t][r] = 0.0f;
   float m_run = -INFINITY, l_run = 0.0f;
-  const float c = a.scale_log2;
   const bf16x2 ones = as_bf16x2(0x3f803f80u);
 
   bf16x8 qf[NDS];  // Q^T B operands, read from LDS at tile 0
