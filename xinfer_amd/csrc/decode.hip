@@ -260,11 +260,12 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     if (it.nsplit == 1) {
       const int g = j % G, i = j / G;
       uint16_t *dst = a.out + it.b * a.o_sb + (int64_t)(it.h * G + g) * a.o_sh + (int64_t)i * a.o_st;
-      dst[d] = (uint16_t)f32_to_bf16_bits(o / lsum);
+      as_global(dst)[d] = (uint16_t)f32_to_bf16_bits(o / lsum);
     } else {
       const int64_t rec = it.rec_begin + ((int64_t)it.h * it.nsplit + it.split) * qrows + j;
-      a.part_o[rec * a.D + d] = o;
-      if (d == 0) *reinterpret_cast<u32x2 *>(a.part_ml + 2 * rec) = u32x2{__float_as_uint(mx), __float_as_uint(lsum)};
+      as_global(a.part_o)[rec * a.D + d] = o;
+      if (d == 0)
+        *as_global(reinterpret_cast<u32x2 *>(a.part_ml + 2 * rec)) = u32x2{__float_as_uint(mx), __float_as_uint(lsum)};
     }
   }
 }

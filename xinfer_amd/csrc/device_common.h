@@ -32,10 +32,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ bf16x2 as_bf16x2(uint32_t w) { return __builtin_bit_cast(bf16x2, w); }
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 w) { return __builtin_bit_cast(bf16x8, w); }
 
-__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
-  return *reinterpret_cast<const u32x4 *>(p);
+// Global-memory pointer of p.  Kernels pin their arguments in SGPRs with an
+// empty asm statement (XATTN_PIN_VIEW below); a pointer that went through it
+// has lost the address space the compiler inferred for kernel arguments, and
+// accesses through it would become flat instructions (which also count
+// against the LDS counter).  as_global() restores the global address space.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *as_global(T *p) {
+  return (__attribute__((address_space(1))) T *)p;
 }
-__device__ __forceinline__ void store16(uint16_t *p, u32x4 v) { *reinterpret_cast<u32x4 *>(p) = v; }
+
+// 16-byte global-memory load and store.
+__device__ __forceinline__ u32x4 load16(const uint16_t *p) {
+  return *as_global(reinterpret_cast<const u32x4 *>(p));
+}
+__device__ __forceinline__ void store16(uint16_t *p, u32x4 v) { *as_global(reinterpret_cast<u32x4 *>(p)) = v; }
 
 // 4-term bf16 dot product of two 8-element bf16 vectors accumulated in fp32.
 __device__ __forceinline__ float dot8_bf16(u32x4 a, u32x4 b, float acc) {

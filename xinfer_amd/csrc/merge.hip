@@ -110,8 +110,8 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
 #pragma unroll
       for (int u = 0; u < INFLIGHT; ++u) {
         const int64_t sp = min(s0 + u * SG, mr.nsplit - 1);
-        ml[u] = *reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step));
-        o[u] = *reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step);
+        ml[u] = *as_global(reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step)));
+        o[u] = *as_global(reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step));
       }
 #pragma unroll
       for (int u = 0; u < INFLIGHT; ++u)
@@ -131,7 +131,7 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   const float inv = 1.0f / st.l;
   const int g = j % G, i = j / G;
   uint16_t *dst = out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st;
-  *reinterpret_cast<u32x2 *>(dst + d) =
+  *as_global(reinterpret_cast<u32x2 *>(dst + d)) =
       u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
 }
 

@@ -492,7 +492,10 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
         }
     } else {
       // Record block of (head, split, tile): [D/4][kTileQ][4] floats, so a
-      // store instruction writes two 512-byte runs of whole cache lines.
+      // store instruction writes two 512-byte runs of whole cache lines.  The
+      // stores are non-temporal: the records stream out while the other items
+      // still compute, instead of waiting in L2 for the write-back at the end
+      // of the launch (the merge launch reads them back either way).
       const int jr = j - tile * kTileQ;
       const int64_t blk = rs.rec_begin + (((int64_t)h * rs.nsplit + split) * rs.ntiles + tile) * kTileQ;
       float *po = a.part_o + blk * D;
@@ -503,12 +506,14 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
           for (int r4 = 0; r4 < 4; ++r4) {
             const int d4 = 8 * t + 2 * r4 + half;  // features 4*d4 .. 4*d4+3
             if (d4 * 4 < D)
-              *reinterpret_cast<f32x4 *>(po + (d4 * kTileQ + jr) * 4) =
-                  f32x4{acc[t][r4 * 4 + 0], acc[t][r4 * 4 + 1], acc[t][r4 * 4 + 2], acc[t][r4 * 4 + 3]};
+              __builtin_nontemporal_store(
+                  f32x4{acc[t][r4 * 4 + 0], acc[t][r4 * 4 + 1], acc[t][r4 * 4 + 2], acc[t][r4 * 4 + 3]},
+                  reinterpret_cast<f32x4 *>(po + (d4 * kTileQ + jr) * 4));
           }
         }
       if (half == 0 && khalf == 0)
-        *reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)) = u32x2{__float_as_uint(m_run), __float_as_uint(l_run)};
+        __builtin_nontemporal_store(u32x2{__float_as_uint(m_run), __float_as_uint(l_run)},
+                                    reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)));
     }
   }
 }
