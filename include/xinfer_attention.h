@@ -92,8 +92,9 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
  *
  * cache_key[r,h,positions[r,t],:] = key[r,h,t,:] (same for value) for
  * t < count_r = cu_query[r+1] - cu_query[r]; positions of padded tokens are
- * never read.  positions: device int64 [B,T] with strides (pos_stride_b,
- * pos_stride_t); cu_query: device int32 [B+1].  Caches are contiguous
+ * not used (they are loaded with the rest, so every one of the B*T entries
+ * must be readable).  positions: device int64 [B,T] with strides
+ * (pos_stride_b, pos_stride_t); cu_query: device int32 [B+1].  Caches are contiguous
  * [B,Hkv,C,D] bf16 and are the only memory written.  A position outside
  * [0, C) is skipped instead of being written out of bounds.
  * ------------------------------------------------------------------------- */

@@ -15,7 +15,7 @@ def append_kv_batched(key, value, positions, cu_query, cache_key, cache_value):
     ``key``/``value``: bf16 [B,Hkv,T,D] (any strides); ``positions``: int64
     [B,T]; ``cu_query``: int32 [B+1] cumulative real-token counts on the device
     (``cuda_offsets[0]``); caches: contiguous bf16 [B,Hkv,C,D], mutated in place.
-    Positions of padded tokens are never read.  Returns None.
+    Positions of padded tokens are not used.  Returns None.
     """
     import torch
 
