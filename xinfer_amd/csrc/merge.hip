@@ -122,9 +122,16 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
     red[sg][f] = st;
     __syncthreads();
     if (sg != 0) return;
-    for (int k = 1; k < SG; ++k) {
-      const MergeState other = red[k][f];
-      fold(st, other.m, other.l, other.o);
+    // The states are read eight at a time before they are folded (in split
+    // lane order), so the fold waits for one LDS round trip per eight lanes.
+    for (int k0 = 1; k0 < SG; k0 += 8) {
+      MergeState other[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < SG) other[u] = red[k0 + u][f];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < SG) fold(st, other[u].m, other[u].l, other[u].o);
     }
   }
   if (!vvalid || d >= D) return;
