@@ -135,6 +135,35 @@ def test_workspace_size_is_a_pure_host_query(lib):
     assert lib.xinfer_flash_attention_workspace_size(ctypes.byref(q1), ctypes.byref(k1), ctypes.c_int64(100)) == 0
 
 
+def prefill_records(lib, counts, lengths, hq, hkv, d, capacity):
+    """Partial records the planner lays out for a batched prefill call."""
+    q, k = view([len(counts), hq, max(counts), d]), view([len(counts), hkv, capacity, d])
+    offsets = [0]
+    for count in counts:
+        offsets.append(offsets[-1] + count)
+    offsets.append(0)
+    for length in lengths:
+        offsets.append(offsets[-1] + length)
+    host = (ctypes.c_int32 * len(offsets))(*offsets)
+    bytes_ = lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(q), ctypes.byref(k), host)
+    return bytes_ // (d * 4 + 8)
+
+
+def test_prefill_split_choice(lib):
+    """Uniform rows keep about 256 items (4 splits of each 128-vector query
+    tile here); a ragged batch whose rows differ 7x in length is cut finer, so
+    that no single item holds a long row's keys."""
+    # cfg2: one 512-token chunk at offset 1536 -> 64 query tiles x 4 splits x 128 vectors.
+    assert prefill_records(lib, [512], [2048], 16, 8, 128, 4096) == 64 * 4 * 128
+    # The same chunk at offset 15872: still 4 splits (4096 keys each).
+    assert prefill_records(lib, [512], [16384], 16, 8, 128, 16384) == 64 * 4 * 128
+    # cfg5 (D = 256, ragged): 300 query tiles; the 9315-key row is split too.
+    counts = [356, 138, 422, 459, 325, 298, 113, 124]
+    lengths = [14244, 13896, 2059, 4214, 12262, 14086, 12837, 9315]
+    tiles = sum(4 * -(-count * 4 // 128) for count in counts)
+    assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) > 3 * tiles * 128
+
+
 def test_operator_schemas_tags_and_fakes(library_path):
     from xinfer_amd.attention import attention_c_shims, cache_extent, load_attention_ops
 

@@ -8,6 +8,7 @@
 // schedule is a function of the shapes and lengths only, never of tensor data,
 // so results are deterministic and each row is isolated from the others'
 // contents.
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 #include <vector>
@@ -21,7 +22,6 @@ namespace {
 
 constexpr int kDecodeMaxQueryVectors = 8;  // G * count at or below this: decode kernel
 constexpr int kPrefillTileQ = 128;         // query vectors per prefill work item
-constexpr int64_t kPrefillTargetItems = 256;
 constexpr int64_t kPrefillMinSplitKeys = 512;
 
 int padded_dim(int64_t d) { return d <= 64 ? 64 : (d <= 128 ? 128 : 256); }
@@ -80,6 +80,120 @@ struct Plan {
   size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
 };
 
+// Measured prefill costs on one MI355X CU, for the planner's choice of split
+// size: one 64-key tile of a 128-vector item (D <= 128: 8 waves, two per
+// SIMD; D = 256: 4 waves), and an item's fixed prologue, fold and epilogue.
+double prefill_tile_us(int dp) { return dp <= 64 ? 0.9 : (dp <= 128 ? 1.15 : 3.2); }
+constexpr double kPrefillItemUs = 4.5;
+// Merge launch: fixed cost, and the record read at about 5 TB/s.
+constexpr double kMergeLaunchUs = 5.0;
+constexpr double kRecordBytesPerUs = 5.0e6;
+constexpr int kCusPerXcd = 32;
+
+// 64-key tiles of prefill item (split, query tile) of row rs: the key range
+// of prefill.hip's split_range for that tile.
+int64_t prefill_item_tiles(const RowSched &rs, int G, int split, int tile) {
+  const int64_t qrows = (int64_t)rs.count * G, p0 = rs.length - rs.count;
+  const int64_t j_last = std::min<int64_t>((int64_t)(tile + 1) * kPrefillTileQ, qrows) - 1;
+  const int64_t kend = p0 + j_last / G + 1;
+  const int64_t per = ceil_div(ceil_div(kend, rs.nsplit), 64) * 64;
+  const int64_t ks0 = std::min(kend, split * per), ks1 = std::min(kend, ks0 + per);
+  return ceil_div(ks1 - ks0, 64);
+}
+
+// Work of every prefill item of rows[0, nrows), in item order (row, kv head,
+// split, query tile), in microseconds.
+std::vector<double> prefill_item_work(const RowSched *rows, int nrows, int64_t Hkv, int G, int dp) {
+  std::vector<double> work;
+  for (int r = 0; r < nrows; ++r) {
+    const RowSched &rs = rows[r];
+    for (int64_t h = 0; h < Hkv; ++h)
+      for (int split = 0; split < rs.nsplit; ++split)
+        for (int tile = 0; tile < rs.ntiles; ++tile)
+          work.push_back(prefill_item_tiles(rs, G, split, tile) * prefill_tile_us(dp) + kPrefillItemUs);
+  }
+  return work;
+}
+
+// Cut items (in order) into 8 contiguous runs of about equal work, one per
+// XCD: on a ragged batch an equal number of items per XCD can leave the XCDs
+// that hold the long rows with most of the work.  begin[0..8].
+void xcd_runs(const std::vector<double> &work, int32_t *begin) {
+  double total = 0;
+  for (double w : work) total += w;
+  begin[0] = 0;
+  size_t i = 0;
+  double done = 0;  // work of items [0, i)
+  for (int x = 1; x < 8; ++x) {
+    const double target = total * x / 8;
+    // Take item i while that lands closer to the target than stopping before it.
+    while (i < work.size() && (done + work[i]) - target < target - done) done += work[i++];
+    begin[x] = (int32_t)i;
+  }
+  begin[8] = (int32_t)work.size();
+}
+
+// Time of the prefill launch when the items run as the hardware dispatches
+// them: the blocks of each XCD, in order, to whichever of its CUs is free.
+double simulated_prefill_us(const std::vector<double> &work) {
+  int32_t begin[9];
+  xcd_runs(work, begin);
+  double span = 0;
+  for (int x = 0; x < 8; ++x) {
+    std::vector<double> free_at(kCusPerXcd, 0.0);
+    for (int32_t i = begin[x]; i < begin[x + 1]; ++i) {
+      auto cu = std::min_element(free_at.begin(), free_at.end());
+      *cu += work[(size_t)i];
+    }
+    span = std::max(span, *std::max_element(free_at.begin(), free_at.end()));
+  }
+  return span;
+}
+
+// Split count of a prefill row for keys-per-split `split_keys`.
+int32_t prefill_splits(int64_t len, int64_t split_keys) {
+  return (int32_t)std::max<int64_t>(1, ceil_div(len, split_keys));
+}
+
+// Keys per prefill split for the call: among splits that give about 256,
+// 512, 1024 or 2048 items (at least kPrefillMinSplitKeys keys), the one whose
+// launch, simulated as dispatched, plus its merge launch, is fastest.  More,
+// smaller items even out ragged rows; they cost per-item overhead, records
+// and merge traffic.
+int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
+                          const std::vector<int32_t> &lengths, int G, int dp) {
+  int64_t prefill_keys = 0;
+  std::vector<RowSched> rows;
+  for (int64_t r = 0; r < g.B; ++r) {
+    const int64_t qv = (int64_t)counts[r] * G;
+    if (qv <= kDecodeMaxQueryVectors) continue;
+    prefill_keys += g.Hkv * ceil_div(qv, kPrefillTileQ) * lengths[r];
+    RowSched rs{};
+    rs.count = counts[r];
+    rs.length = lengths[r];
+    rs.ntiles = (int32_t)ceil_div(qv, kPrefillTileQ);
+    rows.push_back(rs);
+  }
+  int64_t best_keys = kPrefillMinSplitKeys;
+  double best_us = 0;
+  for (int64_t target = 256; target <= 2048; target *= 2) {
+    const int64_t split_keys =
+        std::max(kPrefillMinSplitKeys, ceil_div(ceil_div(prefill_keys, target), 64) * 64);
+    int64_t records = 0;
+    for (RowSched &rs : rows) {
+      rs.nsplit = prefill_splits(rs.length, split_keys);
+      if (rs.nsplit > 1) records += g.Hkv * rs.nsplit * rs.ntiles * kPrefillTileQ;
+    }
+    double us = simulated_prefill_us(prefill_item_work(rows.data(), (int)rows.size(), g.Hkv, G, dp));
+    if (records) us += kMergeLaunchUs + (double)records * (dp * 4 + 8) / kRecordBytesPerUs;
+    if (target == 256 || us < best_us) {
+      best_us = us;
+      best_keys = split_keys;
+    }
+  }
+  return best_keys;
+}
+
 // counts/lengths: per-row real queries and populated KV lengths (validated).
 Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std::vector<int32_t> &lengths) {
   Plan plan;
@@ -88,13 +202,7 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
   const int dp = padded_dim(g.D);
 
   // Keys per prefill split, chosen from the whole call's prefill work.
-  int64_t prefill_keys = 0;
-  for (int64_t r = 0; r < g.B; ++r) {
-    const int64_t qv = (int64_t)counts[r] * G;
-    if (qv > kDecodeMaxQueryVectors) prefill_keys += g.Hkv * ceil_div(qv, kPrefillTileQ) * lengths[r];
-  }
-  int64_t split_keys = ceil_div(ceil_div(prefill_keys, kPrefillTargetItems), 64) * 64;
-  if (split_keys < kPrefillMinSplitKeys) split_keys = kPrefillMinSplitKeys;
+  const int64_t split_keys = choose_split_keys(g, counts, lengths, G, dp);
 
   for (int64_t row0 = 0; row0 < g.B; row0 += kMaxRows) {
     Group grp;
@@ -124,7 +232,7 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
         grp.dec_items += (int)(g.Hkv * rs.nsplit);
       } else {
         rs.ntiles = (int32_t)ceil_div(qv, kPrefillTileQ);
-        rs.nsplit = (int32_t)std::max<int64_t>(1, ceil_div(len, split_keys));
+        rs.nsplit = prefill_splits(len, split_keys);
         rs.item_begin = grp.pre_items;
         grp.pre_items += (int)(g.Hkv * rs.ntiles * rs.nsplit);
       }
@@ -180,8 +288,10 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
     grp.pre.total_items = grp.pre_items;
     if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
-    if (grp.pre_items > 0 && launch_prefill(grp.pre, dp, grp.pre_items, stream) != hipSuccess)
-      return XINFER_ERR_LAUNCH;
+    if (grp.pre_items > 0) {
+      xcd_runs(prefill_item_work(grp.pre.rows, grp.pre.nrows, g.Hkv, G, dp), grp.pre.xcd_begin);
+      if (launch_prefill(grp.pre, dp, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
+    }
     if (grp.merge_items > 0) {
       MergeArgs &m = grp.merge;
       m.out = static_cast<uint16_t *>(out);

@@ -38,6 +38,10 @@ struct AttnArgs {
   int32_t total_items;       // work items of this launch (the decode grid may be smaller)
   int32_t nrows;
   RowSched rows[kMaxRows];
+  // Prefill: items [xcd_begin[x], xcd_begin[x + 1]) run on XCD x (block b
+  // runs item xcd_begin[b % 8] + b / 8 while below xcd_begin[b % 8 + 1]).
+  // The planner cuts the item list into 8 runs of about equal work.
+  int32_t xcd_begin[9];
 };
 
 // Merge of split partial records (merge.hip): one work item per query vector.

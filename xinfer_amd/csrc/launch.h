@@ -14,7 +14,7 @@ hipError_t launch_append(const AppendArgs &a, bool vector, hipStream_t stream);
 int decode_tokens_per_item(int dp, int qr);
 hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int items, hipStream_t stream);
 
-hipError_t launch_prefill(const AttnArgs &a, int dp, int items, hipStream_t stream);
+hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream);
 
 // Merges a.total_items query vectors; max_splits picks the thread layout.
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream);

@@ -170,20 +170,21 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // the late load.
   RowLookup<RowSched> rows;
   rows.load(a.rows);
-  int total_items = a.total_items, nrows = a.nrows, G = a.G, D = a.D, T = a.T;
+  // The hardware hands consecutive blocks to the 8 XCDs in turn.  Block b
+  // runs item xcd_begin[b % 8] + b / 8, so each XCD gets a contiguous run of
+  // items, of about equal work; items are ordered (row, head, split, tile), so
+  // the tiles that read the same keys share that XCD's L2.
+  const int xcd = (int)(blockIdx.x % 8);
+  int run_begin = a.xcd_begin[xcd], run_end = a.xcd_begin[xcd + 1], nrows = a.nrows, G = a.G, D = a.D,
+      T = a.T;
   float c = a.scale_log2;
   View qv = a.q, kv = a.k, vv = a.v;
   asm volatile(""
-               : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(total_items), "+s"(nrows), "+s"(G),
-                 "+s"(D), "+s"(T), "+s"(c), XATTN_PIN_VIEW(qv), XATTN_PIN_VIEW(kv), XATTN_PIN_VIEW(vv));
-  // The hardware hands consecutive blocks to the 8 XCDs in turn.  Block b runs
-  // item (b % 8) * (grid / 8) + b / 8, so each XCD gets a contiguous run of
-  // items; items are ordered (row, head, split, tile), so the tiles that read
-  // the same keys share that XCD's L2.
-  // The grid is total_items rounded up to a multiple of 8 (launch_prefill).
-  const int nblocks = (total_items + 7) / 8 * 8;
-  const int item = (int)(blockIdx.x % 8) * (nblocks / 8) + (int)(blockIdx.x / 8);
-  if (item >= total_items) return;
+               : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(run_begin), "+s"(run_end),
+                 "+s"(nrows), "+s"(G), "+s"(D), "+s"(T), "+s"(c), XATTN_PIN_VIEW(qv), XATTN_PIN_VIEW(kv),
+                 XATTN_PIN_VIEW(vv));
+  const int item = run_begin + (int)(blockIdx.x / 8);
+  if (item >= run_end) return;
   const RowSched rs = rows.find(a.rows, nrows, item);
   const int local = item - rs.item_begin;
   const int per_head = rs.ntiles * rs.nsplit;
@@ -518,10 +519,15 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   }
 }
 
-// Blocks per launch: the item count rounded up to a multiple of the 8 XCDs
-// (blocks past the last item exit at once).
-hipError_t launch_prefill(const AttnArgs &a, int dp, int items, hipStream_t stream) {
-  const dim3 grid((items + 7) / 8 * 8);
+// Blocks per launch: 8 times the longest XCD run (blocks past their run exit
+// at once).
+hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream) {
+  int longest = 0;
+  for (int x = 0; x < 8; ++x) {
+    const int run = a.xcd_begin[x + 1] - a.xcd_begin[x];
+    longest = run > longest ? run : longest;
+  }
+  const dim3 grid(8 * longest);
   switch (dp) {
     case 64: hipLaunchKernelGGL((prefill_kernel<64, 2>), grid, dim3(512), 0, stream, a); break;
     case 128: hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, dim3(512), 0, stream, a); break;
