@@ -76,7 +76,10 @@ def build(verbose: bool = False, jobs: int | None = None) -> Path:
     common = ["-O3", "-fPIC", "-std=c++17", f"-I{ROOT / 'include'}", f"-I{CSRC}"]
     # Host-only translation units still use the HIP runtime API headers.
     host = [f"-isystem{rocm_path() / 'include'}", "-D__HIP_PLATFORM_AMD__"]
-    device = [f"--offload-arch={ARCH}", *NO_PACKED_FP32, "-ffp-contract=fast"]
+    # MFMA accumulators in VGPRs: left to its heuristics, the compiler put the
+    # D = 256 prefill accumulators in AGPRs and copied all 128 of them to
+    # VGPRs and back on every tile.
+    device = [f"--offload-arch={ARCH}", *NO_PACKED_FP32, "-ffp-contract=fast", "-mllvm", "-amdgpu-mfma-vgpr-form=1"]
     torch_flags = [f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *(f"-isystem{p}" for p in torch_includes),
                    f"-isystem{sysconfig.get_paths()['include']}", "-DTORCH_EXTENSION_NAME=xinfer_attention_ops",
                    # torch is built with GCC: keep the Itanium mangling GCC uses for constrained templates.

@@ -116,8 +116,9 @@ __device__ __forceinline__ void wait_lds_and_barrier() {
 }
 
 // Key range [ks0, ks1) of split `split` for a tile whose last visible key is kend-1.
+template <int BN>
 __device__ __forceinline__ void split_range(int kend, int nsplit, int split, int &ks0, int &ks1) {
-  const int per = ((kend + nsplit - 1) / nsplit + kBN - 1) / kBN * kBN;
+  const int per = ((kend + nsplit - 1) / nsplit + BN - 1) / BN * BN;
   ks0 = min(kend, split * per);
   ks1 = min(kend, ks0 + per);
 }
@@ -128,18 +129,24 @@ struct PrefillShape {
   static constexpr int NDS = DP / 16;                 // k-steps of the QK product
   static constexpr int NDT = DP / 32;                 // 32-row d tiles of the output
   static constexpr int CHUNKS = DP / 8;               // 16-byte chunks per key row
-  static constexpr int TILE = kBN * DP;               // bf16 elements of one K (or V) tile
-  static constexpr int LOADS = kBN * CHUNKS / THREADS;  // 16-byte loads per thread per K (or V) tile
+  // D = 256 keeps the query tile in LDS for the whole item and reads its Qᵀ
+  // operands from there (held in registers they would leave no room for the
+  // 128 accumulator registers), over 32-key tiles.
+  static constexpr bool QLDS = DP == 256;
+  static constexpr int BN = QLDS ? 32 : kBN;          // keys per tile
+  static constexpr int TILE = BN * DP;                // bf16 elements of one K (or V) tile
+  static constexpr int LOADS = BN * CHUNKS / THREADS;  // 16-byte loads per thread per K (or V) tile
+  static constexpr int QBYTES = QLDS ? kTileQ * DP * 2 : 0;  // resident query tile
   // Tiles per barrier window (WIN) and LDS stages (K+V of a tile: 4*TILE
   // bytes): two-tile windows over a ring of four stages when it fits in
-  // 128 KB, else one tile per barrier over a ring of 3 (or 2) stages.
-  static constexpr int WIN = 4 * TILE * 4 <= 128 * 1024 ? 2 : 1;
-  static constexpr int NST = WIN == 2 ? 4 : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2);
-  static constexpr int KPW = kBN / KH;                // keys of each tile per wave
+  // 128 KB, else one tile per barrier over a ring of as many stages as fit.
+  static constexpr int WIN = !QLDS && 4 * TILE * 4 <= 128 * 1024 ? 2 : 1;
+  static constexpr int NST = WIN == 2 ? 4 : (QLDS ? (160 * 1024 - QBYTES) / (4 * TILE) : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2));
+  static constexpr int KPW = BN / KH;                 // keys of each tile per wave
   static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
   static constexpr int HALF_T = KH > 1 ? NDT / 2 : NDT;  // d tiles each wave finishes
   static constexpr int FOLD = KH > 1 ? 8 * (HALF_T * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
-  static constexpr int SMEM = (NST * 4 * TILE > FOLD ? NST * 4 * TILE : FOLD);
+  static constexpr int SMEM = (NST * 4 * TILE + QBYTES > FOLD ? NST * 4 * TILE + QBYTES : FOLD);
 };
 
 // XOR swizzles of the 16-byte chunks of a key row (chunk c of key k is stored
@@ -157,7 +164,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   using S = PrefillShape<DP, KH>;
   constexpr int THREADS = S::THREADS, NDS = S::NDS, NDT = S::NDT, CHUNKS = S::CHUNKS;
   constexpr int TILE = S::TILE, LOADS = S::LOADS, NST = S::NST, KPW = S::KPW, NKT = S::NKT;
-  static_assert(LOADS >= 1 && kBN * CHUNKS == LOADS * THREADS, "tile = whole load instructions");
+  static_assert(LOADS >= 1 && S::BN * CHUNKS == LOADS * THREADS, "tile = whole load instructions");
   __shared__ __attribute__((aligned(16))) uint16_t smem[S::SMEM / 2];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -207,8 +214,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int j_last = min(tile * kTileQ + kTileQ, qrows) - 1;
   const int kend = p0 + j_last / G + 1;
   int ks0, ks1;
-  split_range(kend, rs.nsplit, split, ks0, ks1);
-  const int ntile = (ks1 - ks0 + kBN - 1) / kBN;
+  constexpr int BN = S::BN;
+  split_range<BN>(kend, rs.nsplit, split, ks0, ks1);
+  const int ntile = (ks1 - ks0 + BN - 1) / BN;
 
   // This lane's query vector.
   const int j = tile * kTileQ + qgroup * 32 + col;
@@ -242,10 +250,12 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // holds query vector j, swizzled like K.  Rows past the tile's queries and
   // features past D load as zero (an offset past the descriptor's range).
   constexpr int QLOADS = kTileQ * CHUNKS / THREADS;
-  static_assert(kTileQ * CHUNKS == QLOADS * THREADS && kTileQ * DP <= 2 * TILE, "query tile fits a stage");
+  static_assert(kTileQ * CHUNKS == QLOADS * THREADS && (S::QLDS || kTileQ * DP <= 2 * TILE),
+                "query tile fits a stage");
+  uint16_t *const qtile = smem + (S::QLDS ? NST * 2 * TILE : (NST - 1) * 2 * TILE);
   auto issue_query = [&]() {
     const u32x4 q_rsrc = buffer_words(qv.p + b * qv.sb + (int64_t)(h * G) * qv.sh, 0x7fffffffu);
-    uint16_t *qdst = smem + (NST - 1) * 2 * TILE;
+    uint16_t *qdst = qtile;
 #pragma unroll
     for (int i = 0; i < QLOADS; ++i) {
       const int qs = (wave * QLOADS + i) * 64 + lane;
@@ -300,14 +310,43 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     const int kw = kb + khalf * KPW;  // first key of this wave's share
     if (!(wave_active && kw <= wave_kmax && kw < ks1)) return;
     f32x16 s[NKT];
+    if constexpr (S::QLDS) {
+      // Qᵀ operands come from the resident query tile: this wave's rows are
+      // stored with the same swizzle as the K rows of its lanes, so both take
+      // the offsets k_off.  Operands are read in groups of two k-steps, one
+      // group ahead of the MFMAs, and the scheduler may not hoist further:
+      // the 128 accumulator registers leave no room for more.
+      static_assert(KH == 1 && NKT == 1, "query tile in LDS: one key slice of 32-key tiles");
+      const uint16_t *Qw = qtile + qgroup * 32 * DP;
+      constexpr int GR = 2;
+      u32x4 ka[2][GR], qa[2][GR];
+      auto load = [&](int g, int buf) {
 #pragma unroll
-    for (int kt = 0; kt < NKT; ++kt) {
+        for (int u = 0; u < GR; ++u) {
+          ka[buf][u] = *reinterpret_cast<const u32x4 *>(Kt + k_off[g * GR + u]);
+          qa[buf][u] = *reinterpret_cast<const u32x4 *>(Qw + k_off[g * GR + u]);
+        }
+      };
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+      for (int r = 0; r < 16; ++r) s[0][r] = 0.0f;
+      load(0, 0);
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) {
-        const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
-        s[kt] = mfma32(ka, qf[ds], s[kt]);
+      for (int g = 0; g < NDS / GR; ++g) {
+        if (g + 1 < NDS / GR) load(g + 1, (g + 1) & 1);
+#pragma unroll
+        for (int u = 0; u < GR; ++u) s[0] = mfma32(as_bf16x8(ka[g & 1][u]), as_bf16x8(qa[g & 1][u]), s[0]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
+#pragma unroll
+        for (int ds = 0; ds < NDS; ++ds) {
+          const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
+          s[kt] = mfma32(ka, qf[ds], s[kt]);
+        }
       }
     }
     // Mask keys past this column's causal limit or past the split.
@@ -359,6 +398,33 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     // O^T += V^T P^T.  B element e of k-step (kt, hh) is S^T register hh*8+e:
     // key 32kt + 16hh + 8(e/4) + 4half + e%4, i.e. two runs of 4 keys, which the
     // two transposing reads of each A operand supply.
+    if constexpr (S::QLDS) {
+      // V operands in groups of two d tiles, one group ahead (as for QK).
+      constexpr int GT = 2;
+      u32x4 va[2][GT][2];
+      auto load = [&](int g, int buf) {
+#pragma unroll
+        for (int u = 0; u < GT; ++u)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            const uint16_t *vp = Vt + v_off[g * GT + u] + hh * 16 * DP;
+            const u32x2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * DP);
+            va[buf][u][hh] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          }
+      };
+      load(0, 0);
+#pragma unroll
+      for (int g = 0; g < NDT / GT; ++g) {
+        if (g + 1 < NDT / GT) load(g + 1, (g + 1) & 1);
+#pragma unroll
+        for (int u = 0; u < GT; ++u)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+            acc[g * GT + u] = mfma32(as_bf16x8(va[g & 1][u][hh]), pb[0][hh], acc[g * GT + u]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
 #pragma unroll
     for (int t = 0; t < NDT; ++t)
 #pragma unroll
@@ -375,11 +441,12 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // a second barrier frees its buffer (the last stage).
   constexpr int PER_TILE = 2 * LOADS;  // load instructions per tile per thread
   auto read_query = [&]() {
-    const uint16_t *Qt = smem + (NST - 1) * 2 * TILE;
+    if constexpr (!S::QLDS) {
 #pragma unroll
-    for (int ds = 0; ds < NDS; ++ds)
-      qf[ds] = as_bf16x8(
-          *reinterpret_cast<const u32x4 *>(Qt + jr0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+      for (int ds = 0; ds < NDS; ++ds)
+        qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qtile + jr0 * DP +
+                                                             (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+    }
     wait_lds_and_barrier();
   };
   if constexpr (S::WIN == 2) {
@@ -391,7 +458,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     if (ntile > 0) {
       issue_query();
       issue(0, ks0);
-      if (ntile > 1) issue(1, ks0 + kBN);
+      if (ntile > 1) issue(1, ks0 + BN);
     }
     for (int t0 = 0; t0 < ntile; t0 += 4) {
 #pragma unroll
@@ -400,10 +467,10 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
         if (t < ntile) {
           wait_loads_and_barrier<0>();
           if (t == 0) read_query();
-          if (t + 2 < ntile) issue((2 * w + 2) % 4, ks0 + (t + 2) * kBN);
-          if (t + 3 < ntile) issue((2 * w + 3) % 4, ks0 + (t + 3) * kBN);
-          compute(2 * w, ks0 + t * kBN);
-          if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * kBN);
+          if (t + 2 < ntile) issue((2 * w + 2) % 4, ks0 + (t + 2) * BN);
+          if (t + 3 < ntile) issue((2 * w + 3) % 4, ks0 + (t + 3) * BN);
+          compute(2 * w, ks0 + t * BN);
+          if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * BN);
         }
       }
     }
@@ -416,25 +483,24 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       issue_query();
 #pragma unroll
       for (int st = 0; st < NST - 1; ++st)
-        if (st < ntile) issue(st, ks0 + st * kBN);
+        if (st < ntile) issue(st, ks0 + st * BN);
     }
-    for (int t0 = 0; t0 < ntile; t0 += NST) {
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const int t = t0 + st;
-        if (t < ntile) {
-          const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
-          if constexpr (NST == 3) {
-            if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
-            else wait_loads_and_barrier<0>();
-          } else {
-            wait_loads_and_barrier<0>();
-          }
-          if (t == 0) read_query();
-          if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * kBN);
-          compute(st, ks0 + t * kBN);
-        }
+    // Not unrolled over the stages: one instance of the tile's code keeps the
+    // accumulators in the same registers across iterations (unrolled copies
+    // made the compiler move all of them at every back edge).
+#pragma unroll 1
+    for (int t = 0; t < ntile; ++t) {
+      const int st = t % NST;
+      const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
+      if constexpr (NST == 3) {
+        if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
+        else wait_loads_and_barrier<0>();
+      } else {
+        wait_loads_and_barrier<0>();
       }
+      if (t == 0) read_query();
+      if (t + NST - 1 < ntile) issue((t + NST - 1) % NST, ks0 + (t + NST - 1) * BN);
+      compute(st, ks0 + t * BN);
     }
   }
 
