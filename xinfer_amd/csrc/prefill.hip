@@ -485,22 +485,23 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       for (int st = 0; st < NST - 1; ++st)
         if (st < ntile) issue(st, ks0 + st * BN);
     }
-    // Not unrolled over the stages: one instance of the tile's code keeps the
-    // accumulators in the same registers across iterations (unrolled copies
-    // made the compiler move all of them at every back edge).
-#pragma unroll 1
-    for (int t = 0; t < ntile; ++t) {
-      const int st = t % NST;
-      const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
-      if constexpr (NST == 3) {
-        if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
-        else wait_loads_and_barrier<0>();
-      } else {
-        wait_loads_and_barrier<0>();
+    for (int t0 = 0; t0 < ntile; t0 += NST) {
+#pragma unroll
+      for (int st = 0; st < NST; ++st) {
+        const int t = t0 + st;
+        if (t < ntile) {
+          const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
+          if constexpr (NST == 3) {
+            if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
+            else wait_loads_and_barrier<0>();
+          } else {
+            wait_loads_and_barrier<0>();
+          }
+          if (t == 0) read_query();
+          if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * BN);
+          compute(st, ks0 + t * BN);
+        }
       }
-      if (t == 0) read_query();
-      if (t + NST - 1 < ntile) issue((t + NST - 1) % NST, ks0 + (t + NST - 1) * BN);
-      compute(st, ks0 + t * BN);
     }
   }
 
