@@ -399,6 +399,75 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
     return result
 
 
+def measure_norm_rope(index, seed, iters=200):
+    """The fused step before the attention operator (xinfer::qk_norm_rope_append)
+    against the reference adapter's eager modules (transformers Qwen3RMSNorm,
+    apply_rotary_pos_emb, then the append), on one workload's token shape.
+
+    Both are timed as eager launch loops with HIP events on the current stream
+    (the eager sequence is about ten kernels; the fused step is one).  Bytes
+    are algorithmic: the projections, cos/sin and weights read once, the query
+    and the appended key/value rows written once.
+    """
+    import torch
+    from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
+    from xinfer_amd import workloads
+    from xinfer_amd.norm_rope import qk_norm_rope_append
+
+    w = workloads.config(index, seed)
+    batch, tokens, heads, kv_heads, dim = w.batch, w.tokens, w.heads, w.kv_heads, w.dim
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(batch, tokens, heads, dim, generator=g).to(torch.bfloat16).cuda()
+    k = torch.randn(batch, tokens, kv_heads, dim, generator=g).to(torch.bfloat16).cuda()
+    v = torch.randn_like(k)
+    weights = [torch.ones(dim, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    angle = torch.rand(batch, tokens, dim, generator=g).cuda()
+    cos, sin = angle.cos().to(torch.bfloat16), angle.sin().to(torch.bfloat16)
+    positions = torch.stack([torch.arange(p, p + tokens) for p in w.prefixes]).cuda()
+    cu = torch.tensor([0] + torch.tensor(w.counts).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
+    cache = [torch.zeros(batch, kv_heads, w.capacity, dim, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
+    norms = []
+    for weight in weights:
+        norm = Qwen3RMSNorm(dim, eps=1e-6).to(device="cuda", dtype=torch.bfloat16)
+        with torch.no_grad():
+            norm.weight.copy_(weight)
+        norms.append(norm)
+
+    def fused():
+        qk_norm_rope_append(q, k, v, weights[0], weights[1], 1e-6, cos, sin, positions, cu, cache[0], cache[1])
+
+    def eager():
+        qh = norms[0](q).transpose(1, 2)
+        kh = norms[1](k).transpose(1, 2)
+        qh, kh = apply_rotary_pos_emb(qh, kh, cos, sin)
+        torch.ops.xinfer.append_kv_batched(kh, v.transpose(1, 2), positions, cu, cache[0], cache[1])
+
+    def per_call_us(function):
+        with torch.inference_mode():
+            for _ in range(20):
+                function()
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            for _ in range(iters):
+                function()
+            end.record()
+            end.synchronize()
+        return start.elapsed_time(end) * 1e3 / iters
+
+    fused_us, eager_us = per_call_us(fused), per_call_us(eager)
+    real = sum(w.counts)
+    moved = (batch * tokens * (heads + 2 * kv_heads) * dim * 2 + 2 * batch * tokens * dim * 2 + 2 * dim * 2
+             + batch * tokens * heads * dim * 2 + 2 * real * kv_heads * dim * 2)
+    result = {"workload": w.name, "tokens": batch * tokens, "fused_us": round(fused_us, 2),
+              "eager_modules_us": round(eager_us, 2), "speedup": round(eager_us / fused_us, 2),
+              "bytes": moved, "fused_GBs": round(moved / fused_us / 1e3, 1),
+              "frac_hbm": round(moved / fused_us / 1e3 / HBM_PEAK_GBS, 4)}
+    log(f"[bench] norm/rope/append {w.name}: fused {fused_us:.2f} us, eager modules {eager_us:.2f} us, "
+        f"{moved} B = {moved / fused_us / 1e3:.1f} GB/s")
+    return result
+
+
 COPY_PROBE_BYTES = 256 << 20
 
 
@@ -427,7 +496,8 @@ def main():
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
-    parser.add_argument("--all", action="store_true", help="also measure configs 1, 4, 5 and cfg3 seeds 0-7")
+    parser.add_argument("--all", action="store_true",
+                        help="also measure configs 1, 4, 5, cfg3 seeds 0-7 and the fused norm/rope/append step")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
@@ -491,6 +561,8 @@ def main():
     }
     if extra:
         line["configs"] = extra
+    if args.all:
+        line["norm_rope"] = [measure_norm_rope(2, 0), measure_norm_rope(3, 0)]
     print(json.dumps(line), flush=True)
 
 

@@ -40,7 +40,9 @@ enum {
   XINFER_ERR_LAYOUT = 11,         /* feature stride != 1 or rows not 16-byte aligned */
   XINFER_ERR_CACHE = 12,          /* cache tensors not contiguous [B,H,C,D] / shape mismatch */
   XINFER_ERR_LAUNCH = 13,         /* a HIP kernel launch failed */
-  XINFER_ERR_ARGUMENT = 14        /* null pointer or negative size */
+  XINFER_ERR_ARGUMENT = 14,       /* null pointer or negative size */
+  XINFER_ERR_ROPE_SHAPE = 15,     /* xinfer_qk_norm_rope_append shapes (no reference message) */
+  XINFER_ERR_EPS = 16             /* RMSNorm epsilon not finite and >= 0 (no reference message) */
 };
 
 /* A strided rank-4 view of bf16 device memory, [batch, heads, sequence, dim].
@@ -102,6 +104,31 @@ int xinfer_append_kv_batched(const xinfer_view4 *key, const xinfer_view4 *value,
                              const int64_t *positions, int64_t pos_stride_b, int64_t pos_stride_t,
                              const int32_t *cu_query, const xinfer_view4 *cache_key,
                              const xinfer_view4 *cache_value, void *stream);
+
+/* ---------------------------------------------------------------------------
+ * xinfer::qk_norm_rope_append -- replaces the eager step before the attention
+ * operator, compiler/qwen3/adapters/attention.py:44-51 (q_norm/k_norm, i.e.
+ * transformers Qwen3RMSNorm, then apply_rotary_pos_emb, then
+ * KVCache.update = append_kv_batched, compiler/qwen3/model.py:49-52).
+ *
+ * q [B,Hq,T,D], key/value [B,Hkv,T,D]: projections viewed per head (any
+ * strides with unit feature stride, others divisible by 8, 16-byte aligned);
+ * q_weight/k_weight: the [D] RMSNorm weights; cos/sin [B,1,T,D] (stride[1]
+ * unused): the rotary tables of the tokens; D in {64, 128, 256}.
+ *   xn = bf16(w * bf16(x * rsqrt(mean(x^2) + eps)))   per (token, head) row
+ *   x' = bf16(bf16(xn * cos) + bf16(rotate_half(xn) * sin))
+ * q_out: contiguous [B,Hq,T,D] receives q' for every token.  cache_key
+ * receives k' and cache_value v at [r, h, positions[r,t]] for t < count_r
+ * (count_r, positions and the skipping of positions outside [0, C) as in
+ * xinfer_append_kv_batched).  No reference counterpart in the C ABI: the
+ * reference runs this step as separate eager or compiled PyTorch ops.
+ * ------------------------------------------------------------------------- */
+int xinfer_qk_norm_rope_append(const xinfer_view4 *q, const xinfer_view4 *key, const xinfer_view4 *value,
+                               const void *q_weight, const void *k_weight, double eps,
+                               const xinfer_view4 *cos, const xinfer_view4 *sin, const int64_t *positions,
+                               int64_t pos_stride_b, int64_t pos_stride_t, const int32_t *cu_query,
+                               void *q_out, const xinfer_view4 *cache_key, const xinfer_view4 *cache_value,
+                               void *stream);
 
 /* The AOTInductor C shims of the same library are declared in
  * xinfer_attention_aoti.h. */

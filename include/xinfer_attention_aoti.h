@@ -50,6 +50,17 @@ AOTITorchError aoti_torch_cuda_append_kv_batched(AtenTensorHandle key, AtenTenso
                                                  AtenTensorHandle cache_value,
                                                  AtenTensorHandle *unused_output);
 
+/* New: the fused step before the attention operator (xinfer_qk_norm_rope_append
+ * in xinfer_attention.h), which replaces eager ops of
+ * compiler/qwen3/adapters/attention.py:44-51 that AOTI would otherwise compile
+ * into the wrapper.  Returns the rotated query [B,Hq,T,D] as a new tensor and
+ * mutates cache_key/cache_value in place. */
+AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
+    AtenTensorHandle q, AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle q_weight,
+    AtenTensorHandle k_weight, double eps, AtenTensorHandle cos, AtenTensorHandle sin,
+    AtenTensorHandle positions, AtenTensorHandle cu_query, AtenTensorHandle cache_key,
+    AtenTensorHandle cache_value, AtenTensorHandle *output);
+
 #ifdef __cplusplus
 }
 #endif

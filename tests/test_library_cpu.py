@@ -70,8 +70,9 @@ def lib(library_path):
 def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert {"xinfer_flash_attention", "xinfer_batched_flash_attention", "xinfer_append_kv_batched",
-            "aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
-            "aoti_torch_cuda_append_kv_batched"} <= set(names)
+            "xinfer_qk_norm_rope_append", "aoti_torch_cuda_flash_attention",
+            "aoti_torch_cuda_batched_flash_attention", "aoti_torch_cuda_append_kv_batched",
+            "aoti_torch_cuda_qk_norm_rope_append"} <= set(names)
     for name in names:
         assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
 
@@ -119,6 +120,32 @@ def test_batched_validation_codes(lib):
     assert batched(lib, q, k, [0, 3, 4, 0, 2, 9]) == 9   # length < count
     assert batched(lib, q, k, [0, 1, 2, 0, 65, 70]) == 9  # length > capacity
     assert batched(lib, q, k, [0, 1, 2, 0, 5, 9], scale=0.0) == 7
+
+
+def norm_rope(lib, q, k, rope, cache, eps=1e-6, cu_query=1 << 21):
+    return lib.xinfer_qk_norm_rope_append(
+        ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), ctypes.c_void_p(1 << 22), ctypes.c_void_p(1 << 22),
+        ctypes.c_double(eps), ctypes.byref(rope), ctypes.byref(rope), ctypes.c_void_p(1 << 23), ctypes.c_int64(4),
+        ctypes.c_int64(1), ctypes.c_void_p(cu_query), ctypes.c_void_p(1 << 24), ctypes.byref(cache),
+        ctypes.byref(cache), None)
+
+
+def test_norm_rope_validation_codes(lib):
+    """Every rejected input returns before any launch (no device is touched)."""
+    q, k, rope, cache = view([2, 16, 4, 128]), view([2, 8, 4, 128]), view([2, 1, 4, 128]), view([2, 8, 64, 128])
+    assert lib.xinfer_status_string(15).decode().startswith("Expected q [B,Hq,T,D]")
+    assert lib.xinfer_status_string(16).decode() == "RMSNorm epsilon must be finite and non-negative"
+    assert norm_rope(lib, view([2, 16, 4, 96]), view([2, 8, 4, 96]), view([2, 1, 4, 96]), view([2, 8, 64, 96])) == 15
+    assert norm_rope(lib, q, view([2, 8, 5, 128]), rope, cache) == 15
+    assert norm_rope(lib, q, k, view([2, 2, 4, 128]), cache) == 15
+    assert norm_rope(lib, q, k, rope, cache, eps=-1.0) == 16
+    assert norm_rope(lib, q, k, rope, cache, eps=float("nan")) == 16
+    assert norm_rope(lib, view([0, 16, 4, 128]), view([0, 8, 4, 128]), view([0, 1, 4, 128]), cache) == 0
+    assert norm_rope(lib, q, k, rope, cache, cu_query=0) == 14
+    assert norm_rope(lib, view([2, 16, 4, 128], data=(1 << 20) + 2), k, rope, cache) == 11
+    assert norm_rope(lib, view([2, 16, 4, 128], [16 * 4 * 132, 4 * 132, 132, 1]), k, rope, cache) == 11
+    assert norm_rope(lib, q, k, rope, view([2, 8, 64, 128], [8 * 64 * 128, 128, 8 * 128, 1])) == 12
+    assert norm_rope(lib, q, k, rope, view([2, 4, 64, 128])) == 12
 
 
 def test_workspace_size_is_a_pure_host_query(lib):
@@ -174,10 +201,10 @@ def test_operator_schemas_tags_and_fakes(library_path):
     assert torch.Tag.flexible_layout in torch.ops.xinfer.flash_attention.default.tags
     assert torch.Tag.flexible_layout in torch.ops.xinfer.batched_flash_attention.default.tags
     shims = attention_c_shims()
-    assert len(shims) == 3
+    assert len(shims) == 4
     assert all(name in text[0] for name, text in zip(
         ("aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
-         "aoti_torch_cuda_append_kv_batched"), shims.values()))
+         "aoti_torch_cuda_append_kv_batched", "aoti_torch_cuda_qk_norm_rope_append"), shims.values()))
     with FakeTensorMode(allow_non_fake_inputs=True):
         q = torch.empty(2, 16, 3, 128, dtype=torch.bfloat16, device="cuda").transpose(1, 2).contiguous().transpose(1, 2)
         k = torch.empty(2, 8, 64, 128, dtype=torch.bfloat16, device="cuda")

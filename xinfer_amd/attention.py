@@ -9,7 +9,10 @@ which registers three operators in the `xinfer` namespace:
 * ``flash_attention`` and ``batched_flash_attention`` -- read-only attention
   over each request's populated KV prefix (HIP kernels for gfx950);
 * ``append_kv_batched`` -- the in-place KV-cache append, native instead of the
-  reference's Triton op (compiler/common/kernels/kv_cache.py:45-72).
+  reference's Triton op (compiler/common/kernels/kv_cache.py:45-72);
+* ``qk_norm_rope_append`` -- the step before the attention operator in one
+  launch: q/k RMSNorm, rotary embedding and the KV append
+  (compiler/qwen3/adapters/attention.py:44-51), see xinfer_amd/norm_rope.py.
 """
 
 import os
@@ -30,6 +33,12 @@ APPEND_KV_C_SHIM = """AOTITorchError aoti_torch_cuda_append_kv_batched(
     AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle positions,
     AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value,
     AtenTensorHandle* unused_output)"""
+NORM_ROPE_C_SHIM = """AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
+    AtenTensorHandle q, AtenTensorHandle key, AtenTensorHandle value,
+    AtenTensorHandle q_weight, AtenTensorHandle k_weight, double eps,
+    AtenTensorHandle cos, AtenTensorHandle sin, AtenTensorHandle positions,
+    AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value,
+    AtenTensorHandle* output)"""
 MODELS = ("qwen3", "qwen35")
 _loaded = None
 
@@ -138,6 +147,19 @@ def load_attention_ops(library=None, *, model=None):
             torch._check(cache_key.is_contiguous() and cache_value.is_contiguous())
             return None
 
+    if hasattr(torch.ops.xinfer, "qk_norm_rope_append"):
+
+        @torch.library.register_fake("xinfer::qk_norm_rope_append")
+        def fake_norm_rope(q, key, value, q_weight, k_weight, eps, cos, sin, positions, cu_query,
+                           cache_key, cache_value):
+            torch._check(q.dim() == 4 and key.dim() == 4 and value.shape == key.shape)
+            torch._check(key.shape[0] == q.shape[0] and key.shape[1] == q.shape[1])
+            torch._check(key.shape[3] == q.shape[3])
+            torch._check(cos.shape == (q.shape[0], q.shape[1], q.shape[3]) and sin.shape == cos.shape)
+            torch._check(q_weight.shape == (q.shape[3],) and k_weight.shape == q_weight.shape)
+            torch._check(cache_key.is_contiguous() and cache_value.is_contiguous())
+            return q.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
+
     _loaded = library
 
 
@@ -151,7 +173,8 @@ def attention_c_shims():
     """Inductor's call declarations for the registered operators.
 
     The reference maps the two attention operators (attention.py:105-112); the
-    native append needs its own entry because it is no longer a Triton op.
+    native append needs its own entry because it is no longer a Triton op, and
+    so does the fused norm/rope/append step.
     """
     import torch
 
@@ -159,4 +182,5 @@ def attention_c_shims():
         torch.ops.xinfer.flash_attention.default: [ATTENTION_C_SHIM],
         torch.ops.xinfer.batched_flash_attention.default: [BATCHED_ATTENTION_C_SHIM],
         torch.ops.xinfer.append_kv_batched.default: [APPEND_KV_C_SHIM],
+        torch.ops.xinfer.qk_norm_rope_append.default: [NORM_ROPE_C_SHIM],
     }

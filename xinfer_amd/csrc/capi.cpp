@@ -384,6 +384,9 @@ const char *xinfer_status_string(int status) {
       return "Expected contiguous KV caches [batch,kv_heads,capacity,head_dim] matching key/value";
     case XINFER_ERR_LAUNCH: return "HIP kernel launch failed";
     case XINFER_ERR_ARGUMENT: return "Invalid argument";
+    case XINFER_ERR_ROPE_SHAPE:
+      return "Expected q [B,Hq,T,D], key/value [B,Hkv,T,D] and cos/sin [B,1,T,D] with D in {64,128,256}";
+    case XINFER_ERR_EPS: return "RMSNorm epsilon must be finite and non-negative";
     default: return "Unknown xinfer status";
   }
 }
@@ -480,6 +483,70 @@ int xinfer_append_kv_batched(const xinfer_view4 *key, const xinfer_view4 *value,
                       (reinterpret_cast<uintptr_t>(cache_value->data) & 15u) == 0;
   return launch_append(a, vector, static_cast<hipStream_t>(stream)) == hipSuccess ? XINFER_OK
                                                                                   : XINFER_ERR_LAUNCH;
+}
+
+int xinfer_qk_norm_rope_append(const xinfer_view4 *q, const xinfer_view4 *key, const xinfer_view4 *value,
+                               const void *q_weight, const void *k_weight, double eps,
+                               const xinfer_view4 *cos, const xinfer_view4 *sin, const int64_t *positions,
+                               int64_t pos_stride_b, int64_t pos_stride_t, const int32_t *cu_query,
+                               void *q_out, const xinfer_view4 *cache_key, const xinfer_view4 *cache_value,
+                               void *stream) {
+  if (!q || !key || !value || !cos || !sin || !cache_key || !cache_value) return XINFER_ERR_ARGUMENT;
+  const int64_t B = q->size[0], Hq = q->size[1], T = q->size[2], D = q->size[3], Hkv = key->size[1];
+  for (int i = 0; i < 4; ++i)
+    if (q->size[i] < 0 || key->size[i] < 0 || value->size[i] != key->size[i]) return XINFER_ERR_ROPE_SHAPE;
+  if (key->size[0] != B || key->size[2] != T || key->size[3] != D || Hq <= 0 || Hkv <= 0 ||
+      (D != 64 && D != 128 && D != 256))
+    return XINFER_ERR_ROPE_SHAPE;
+  for (const xinfer_view4 *r : {cos, sin})
+    if (r->size[0] != B || r->size[1] != 1 || r->size[2] != T || r->size[3] != D) return XINFER_ERR_ROPE_SHAPE;
+  if (!(std::isfinite(eps) && eps >= 0)) return XINFER_ERR_EPS;
+  if (B == 0 || T == 0) return XINFER_OK;
+  if (!q_weight || !k_weight || !positions || !cu_query || !q_out) return XINFER_ERR_ARGUMENT;
+  // 16-byte rows: unit feature stride, other strides divisible by 8, aligned data.
+  auto rows_ok = [](const xinfer_view4 &t) {
+    if (t.data == nullptr || (reinterpret_cast<uintptr_t>(t.data) & 15u) != 0 || t.stride[3] != 1) return false;
+    for (int i = 0; i < 3; ++i)
+      if (t.size[i] > 1 && t.stride[i] % 8 != 0) return false;
+    return true;
+  };
+  for (const xinfer_view4 *t : {q, key, value, cos, sin})
+    if (!rows_ok(*t)) return XINFER_ERR_LAYOUT;
+  for (const void *p : {q_weight, k_weight, static_cast<const void *>(q_out)})
+    if ((reinterpret_cast<uintptr_t>(p) & 15u) != 0) return XINFER_ERR_LAYOUT;
+  for (const xinfer_view4 *c : {cache_key, cache_value}) {
+    if (!c->data || (reinterpret_cast<uintptr_t>(c->data) & 15u) != 0 || c->size[0] < B || c->size[1] != Hkv ||
+        c->size[3] != D || c->size[2] <= 0)
+      return XINFER_ERR_CACHE;
+    if (c->stride[3] != 1 || c->stride[2] != D || c->stride[1] != c->size[2] * D ||
+        c->stride[0] != Hkv * c->size[2] * D)
+      return XINFER_ERR_CACHE;
+    for (int i = 0; i < 4; ++i)
+      if (c->size[i] != cache_key->size[i]) return XINFER_ERR_CACHE;
+  }
+  NormRopeArgs a{};
+  a.q = view_of(*q);
+  a.k = view_of(*key);
+  a.v = view_of(*value);
+  a.q_weight = static_cast<const uint16_t *>(q_weight);
+  a.k_weight = static_cast<const uint16_t *>(k_weight);
+  a.cos = view_of(*cos);
+  a.sin = view_of(*sin);
+  a.positions = positions;
+  a.pos_sb = pos_stride_b;
+  a.pos_st = pos_stride_t;
+  a.cu_query = cu_query;
+  a.q_out = static_cast<uint16_t *>(q_out);
+  a.cache_key = static_cast<uint16_t *>(const_cast<void *>(cache_key->data));
+  a.cache_value = static_cast<uint16_t *>(const_cast<void *>(cache_value->data));
+  a.eps = (float)eps;
+  a.B = (int32_t)B;
+  a.T = (int32_t)T;
+  a.Hq = (int32_t)Hq;
+  a.Hkv = (int32_t)Hkv;
+  a.D = (int32_t)D;
+  a.C = (int32_t)cache_key->size[2];
+  return launch_norm_rope(a, static_cast<hipStream_t>(stream)) == hipSuccess ? XINFER_OK : XINFER_ERR_LAUNCH;
 }
 
 }  // extern "C"

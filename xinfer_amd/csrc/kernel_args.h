@@ -77,4 +77,18 @@ struct AppendArgs {
   int32_t B, H, T, D, C;
 };
 
+// Query/key RMSNorm + rotary embedding + KV append (norm_rope.hip).
+struct NormRopeArgs {
+  View q, k, v;                        // [B, H, T, D] views of the projections
+  const uint16_t *q_weight, *k_weight;  // [D] RMSNorm weights
+  View cos, sin;                       // [B, T, D] (sb, st; sh unused)
+  const int64_t *positions;
+  int64_t pos_sb, pos_st;
+  const int32_t *cu_query;
+  uint16_t *q_out;                     // contiguous [B, Hq, T, D]
+  uint16_t *cache_key, *cache_value;   // contiguous [B, Hkv, C, D]
+  float eps;
+  int32_t B, T, Hq, Hkv, D, C;
+};
+
 }  // namespace xattn

@@ -8,6 +8,7 @@
 namespace xattn {
 
 hipError_t launch_append(const AppendArgs &a, bool vector, hipStream_t stream);
+hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t stream);
 
 // Keys handled by one decode work item for padded head dim `dp` and `qr` query
 // vectors per KV head (a power of two <= 8).

@@ -184,6 +184,52 @@ void append_kv_batched(const at::Tensor &key, const at::Tensor &value, const at:
                                         static_cast<const int32_t *>(cu.data_ptr()), &ck, &cv, current_stream(key)));
 }
 
+// Replaces the eager step before the attention operator,
+// compiler/qwen3/adapters/attention.py:44-51: q/k RMSNorm (transformers
+// Qwen3RMSNorm), apply_rotary_pos_emb and KVCache.update (the append).
+// q [B,T,Hq,D], key/value [B,T,Hkv,D] are the projections viewed per head
+// (`proj(x).view(B, T, -1, D)`), cos/sin [B,T,D]; returns the rotated query
+// as a contiguous [B,Hq,T,D] tensor and appends the rotated key and the value
+// to the caches in place.
+at::Tensor qk_norm_rope_append(const at::Tensor &q, const at::Tensor &key, const at::Tensor &value,
+                               const at::Tensor &q_weight, const at::Tensor &k_weight, double eps,
+                               const at::Tensor &cos, const at::Tensor &sin, const at::Tensor &positions,
+                               const at::Tensor &cu_query, const at::Tensor &cache_key,
+                               const at::Tensor &cache_value) {
+  TORCH_CHECK(q.dim() == 4 && key.dim() == 4 && value.sizes() == key.sizes() && key.size(0) == q.size(0) &&
+                  key.size(1) == q.size(1) && key.size(3) == q.size(3) && cos.dim() == 3 &&
+                  cos.sizes() == sin.sizes() && cos.size(0) == q.size(0) && cos.size(1) == q.size(1) &&
+                  cos.size(2) == q.size(3) && q_weight.dim() == 1 && q_weight.size(0) == q.size(3) &&
+                  k_weight.sizes() == q_weight.sizes(),
+              "Expected q [B,T,Hq,D], key/value [B,T,Hkv,D], cos/sin [B,T,D] and [D] weights");
+  for (const at::Tensor *t : {&q, &key, &value, &q_weight, &k_weight, &cos, &sin, &cache_key, &cache_value})
+    TORCH_CHECK(t->scalar_type() == at::kBFloat16, "xinfer norm/rope append requires BF16");
+  for (const at::Tensor *t : {&key, &value, &q_weight, &k_weight, &cos, &sin, &positions, &cu_query, &cache_key,
+                              &cache_value})
+    TORCH_CHECK(q.is_cuda() && t->device() == q.device(), "xinfer norm/rope append requires colocated CUDA tensors");
+  TORCH_CHECK(cache_key.is_contiguous() && cache_value.is_contiguous(), "Expected contiguous KV caches");
+  TORCH_CHECK(positions.scalar_type() == at::kLong && positions.dim() == 2 && positions.size(0) == q.size(0) &&
+                  positions.size(1) == q.size(1),
+              "Expected int64 positions [B,T]");
+  TORCH_CHECK(cu_query.scalar_type() == at::kInt && cu_query.dim() == 1 && cu_query.size(0) == q.size(0) + 1,
+              "Expected int32 cumulative query lengths [B+1]");
+  c10::DeviceGuard guard(q.device());
+  auto output = at::empty({q.size(0), q.size(2), q.size(1), q.size(3)}, q.options());
+  // Per-head views [B,H,T,D]; rows the kernel cannot read in place are copied.
+  auto rows = [](const at::Tensor &t) { return kernel_layout(t) ? t : t.contiguous(); };
+  auto qh = rows(q.transpose(1, 2)), kh = rows(key.transpose(1, 2)), vh = rows(value.transpose(1, 2));
+  auto cs = rows(cos.unsqueeze(1)), sn = rows(sin.unsqueeze(1));
+  auto qw = q_weight.contiguous(), kw = k_weight.contiguous();
+  auto cu = cu_query.is_contiguous() ? cu_query : cu_query.contiguous();
+  auto qv = view_of(qh), kv = view_of(kh), vv = view_of(vh), cv = view_of(cs), sv = view_of(sn);
+  auto ck = view_of(cache_key), cvv = view_of(cache_value);
+  check_status(xinfer_qk_norm_rope_append(&qv, &kv, &vv, qw.data_ptr(), kw.data_ptr(), eps, &cv, &sv,
+                                          static_cast<const int64_t *>(positions.data_ptr()), positions.stride(0),
+                                          positions.stride(1), static_cast<const int32_t *>(cu.data_ptr()),
+                                          output.data_ptr(), &ck, &cvv, current_stream(q)));
+  return output;
+}
+
 }  // namespace xinfer
 
 TORCH_LIBRARY(xinfer, m) {
@@ -194,12 +240,16 @@ TORCH_LIBRARY(xinfer, m) {
         {at::Tag::flexible_layout});
   m.def("append_kv_batched(Tensor key, Tensor value, Tensor positions, Tensor cu_query, "
         "Tensor(a4!) cache_key, Tensor(a5!) cache_value) -> ()");
+  m.def("qk_norm_rope_append(Tensor q, Tensor key, Tensor value, Tensor q_weight, Tensor k_weight, "
+        "float eps, Tensor cos, Tensor sin, Tensor positions, Tensor cu_query, Tensor(a10!) cache_key, "
+        "Tensor(a11!) cache_value) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(xinfer, CUDA, m) {
   m.impl("batched_flash_attention", TORCH_FN(xinfer::batched_flash_attention));
   m.impl("flash_attention", TORCH_FN(xinfer::flash_attention));
   m.impl("append_kv_batched", TORCH_FN(xinfer::append_kv_batched));
+  m.impl("qk_norm_rope_append", TORCH_FN(xinfer::qk_norm_rope_append));
 }
 
 using torch::aot_inductor::new_tensor_handle;
@@ -237,6 +287,20 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_append_kv_batched(
                               resolve_tensor_dispatch_flags(cu_query),
                               resolve_tensor_dispatch_flags(cache_key),
                               resolve_tensor_dispatch_flags(cache_value));
+  });
+}
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
+    AtenTensorHandle q, AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle q_weight,
+    AtenTensorHandle k_weight, double eps, AtenTensorHandle cos, AtenTensorHandle sin, AtenTensorHandle positions,
+    AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value, AtenTensorHandle *output) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    *output = new_tensor_handle(xinfer::qk_norm_rope_append(
+        resolve_tensor_dispatch_flags(q), resolve_tensor_dispatch_flags(key), resolve_tensor_dispatch_flags(value),
+        resolve_tensor_dispatch_flags(q_weight), resolve_tensor_dispatch_flags(k_weight), eps,
+        resolve_tensor_dispatch_flags(cos), resolve_tensor_dispatch_flags(sin),
+        resolve_tensor_dispatch_flags(positions), resolve_tensor_dispatch_flags(cu_query),
+        resolve_tensor_dispatch_flags(cache_key), resolve_tensor_dispatch_flags(cache_value)));
   });
 }
 
