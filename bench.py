@@ -1,6 +1,6 @@
 """Benchmark of the xinfer attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--norm-rope] [--no-cpu-baseline]
 
 A step is one pass of the hot path over one batch: the in-place KV append of
 each row's new tokens followed by one attention call over the populated
@@ -498,6 +498,9 @@ def main():
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--all", action="store_true",
                         help="also measure configs 1, 4, 5, cfg3 seeds 0-7 and the fused norm/rope/append step")
+    parser.add_argument("--norm-rope", action="store_true",
+                        help="only time the fused norm/rope/append step against the eager modules and print "
+                             "its JSON (cfg2 and cfg3 token shapes)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
@@ -528,6 +531,9 @@ def main():
     load_attention_ops(os.environ.get("XINFER_ATTENTION_OPS_LIBRARY") or library_path())
     if args.copy_probe:
         copy_probe()
+    if args.norm_rope:
+        print(json.dumps({"norm_rope": [measure_norm_rope(2, 0), measure_norm_rope(3, 0)]}), flush=True)
+        return
     with_cpu = not args.no_cpu_baseline
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
