@@ -88,6 +88,17 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
                                    const xinfer_view4 *v, const int32_t *host_offsets, double scale,
                                    void *out, void *workspace, size_t workspace_bytes, void *stream);
 
+/* Same operation with the output written through a caller-supplied view of
+ * q's sizes [B,Hq,T,D] (unit feature stride, other strides multiples of 8,
+ * 16-byte aligned data), e.g. [B,T,Hq,D] storage viewed as [B,Hq,T,D].  The
+ * workspace is the one *_workspace_size reports.  No reference counterpart:
+ * it serves xinfer::batched_flash_attention_bthd, the optional variant that
+ * spares compiler/qwen3/adapters/attention.py:61 its transpose copy. */
+int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4 *k,
+                                       const xinfer_view4 *v, const int32_t *host_offsets,
+                                       double scale, const xinfer_view4 *out, void *workspace,
+                                       size_t workspace_bytes, void *stream);
+
 /* ---------------------------------------------------------------------------
  * xinfer::append_kv_batched -- replaces the Triton op
  * compiler/common/kernels/kv_cache.py:8-72.

@@ -38,6 +38,14 @@ AOTITorchError aoti_torch_cuda_batched_flash_attention(AtenTensorHandle q, AtenT
                                                        AtenTensorHandle blocks, double scale,
                                                        AtenTensorHandle *output);
 
+/* New, optional: xinfer::batched_flash_attention_bthd, the same operation
+ * with a contiguous [B,T,Hq,D] output (xinfer_batched_flash_attention_out). */
+AOTITorchError aoti_torch_cuda_batched_flash_attention_bthd(AtenTensorHandle q, AtenTensorHandle k,
+                                                            AtenTensorHandle v, AtenTensorHandle offsets,
+                                                            AtenTensorHandle cuda_offsets,
+                                                            AtenTensorHandle blocks, double scale,
+                                                            AtenTensorHandle *output);
+
 /* New: the reference's append is a Triton op (compiler/common/kernels/kv_cache.py:45-72)
  * that AOTI compiles into the wrapper; the native op needs its own shim.  It
  * mutates cache_key/cache_value in place and returns nothing.  AOTInductor's

@@ -189,6 +189,60 @@ def test_long_decode_rows_through_every_merge_layout(gpu_ops):
 
 
 @torch.inference_mode()
+def test_batches_beyond_one_row_table(gpu_ops):
+    """More rows than one launch's row table (64) take several launch groups,
+    each with its own decode, prefill and merge launches over one workspace:
+    a mix of empty, single-token, short and split rows across group borders."""
+    torch.manual_seed(31)
+    op = gpu_ops.batched_flash_attention.default
+    batch = 150
+    pattern = [(0, 9), (1, 700), (3, 40), (20, 300), (1, 5000), (64, 2100), (2, 2)]
+    counts = [pattern[r % len(pattern)][0] for r in range(batch)]
+    lengths = [pattern[r % len(pattern)][1] for r in range(batch)]
+    log(f"batched {batch} rows in {-(-batch // 64)} launch groups")
+    q, k, v = inputs(16, 8, 128, 64, capacity=5000, batch_size=batch)
+    host, cu, blocks = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), q.device
+    )
+    actual = op(q, k, v, host, cu, blocks, 128**-0.5)
+    expected = reference_attention(q, k, v, counts, lengths, 128**-0.5)
+    for row, count in enumerate(counts):
+        assert torch.count_nonzero(actual[row, :, count:]).item() == 0
+    assert_close_rows(actual, expected, counts)
+    assert torch.equal(actual, op(q, k, v, host, cu, blocks, 128**-0.5))
+
+
+@torch.inference_mode()
+def test_bthd_output_variant_equals_the_transposed_output(gpu_ops):
+    """batched_flash_attention_bthd runs the same schedule and arithmetic and
+    only writes through [B,T,Hq,D] strides: bit-identical to the standard
+    operator's output transposed, padded queries zero, for decode rows, split
+    prefill rows and both head dims; the adapter's reshape is then a view."""
+    torch.manual_seed(41)
+    standard = gpu_ops.batched_flash_attention.default
+    bthd = gpu_ops.batched_flash_attention_bthd.default
+    for heads, kv_heads, dim, counts, lengths in (
+        (16, 8, 128, [1, 1, 0, 1], [13312, 386, 9, 55]),
+        (16, 8, 128, [512, 37, 0], [2048, 3000, 1]),
+        (16, 4, 256, [356, 1, 124], [14244, 700, 9315]),
+        (8, 8, 64, [3, 17], [40, 17]),
+    ):
+        log(f"bthd output heads={heads}/{kv_heads} dim={dim} counts={counts} lengths={lengths}")
+        q, k, v = inputs(heads, kv_heads, dim, max(counts), capacity=max(lengths), batch_size=len(counts))
+        host, cu, blocks = batched_attention_metadata(
+            torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), q.device
+        )
+        expected = standard(q, k, v, host, cu, blocks, dim**-0.5)
+        actual = bthd(q, k, v, host, cu, blocks, dim**-0.5)
+        assert actual.shape == (len(counts), max(counts), heads, dim) and actual.is_contiguous()
+        assert torch.equal(actual, expected.transpose(1, 2))
+        flat = actual.reshape(len(counts), max(counts), -1)
+        assert flat.data_ptr() == actual.data_ptr()
+        torch.library.opcheck(bthd, (q, k, v, host, cu, blocks, dim**-0.5),
+                              test_utils=("test_schema", "test_faketensor"))
+
+
+@torch.inference_mode()
 def test_appended_chunks_use_lower_right_causality(gpu_ops):
     op = gpu_ops.flash_attention.default
     for heads, kv_heads, dim in ((16, 8, 128), (8, 2, 256)):

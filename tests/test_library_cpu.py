@@ -70,7 +70,7 @@ def lib(library_path):
 def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert {"xinfer_flash_attention", "xinfer_batched_flash_attention", "xinfer_append_kv_batched",
-            "xinfer_qk_norm_rope_append", "aoti_torch_cuda_flash_attention",
+            "xinfer_qk_norm_rope_append", "xinfer_batched_flash_attention_out", "aoti_torch_cuda_flash_attention",
             "aoti_torch_cuda_batched_flash_attention", "aoti_torch_cuda_append_kv_batched",
             "aoti_torch_cuda_qk_norm_rope_append"} <= set(names)
     for name in names:
@@ -148,6 +148,22 @@ def test_norm_rope_validation_codes(lib):
     assert norm_rope(lib, q, k, rope, view([2, 4, 64, 128])) == 12
 
 
+def test_output_view_validation_codes(lib):
+    """xinfer_batched_flash_attention_out checks its output view before any launch."""
+    q, k = view([2, 16, 4, 128]), view([2, 8, 64, 128])
+    host = (ctypes.c_int32 * 6)(0, 1, 2, 0, 5, 9)
+
+    def call(out):
+        return lib.xinfer_batched_flash_attention_out(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), host,
+                                                      ctypes.c_double(0.1), out, None, ctypes.c_size_t(0), None)
+
+    assert call(None) == 14
+    assert call(ctypes.byref(view([2, 16, 5, 128]))) == 1
+    assert call(ctypes.byref(view([2, 16, 4, 128], data=(1 << 20) + 8))) == 11
+    assert call(ctypes.byref(view([2, 16, 4, 128], [4 * 16 * 128, 128, 16 * 128 + 4, 1]))) == 11
+    assert call(ctypes.byref(view([2, 16, 4, 128], [4 * 16 * 256, 256, 16 * 256, 2]))) == 11
+
+
 def test_workspace_size_is_a_pure_host_query(lib):
     q, k = view([8, 16, 1, 128]), view([8, 8, 16384, 128])
     lengths = [13312, 2162, 386, 9459, 1399, 3852, 55, 182]
@@ -201,10 +217,11 @@ def test_operator_schemas_tags_and_fakes(library_path):
     assert torch.Tag.flexible_layout in torch.ops.xinfer.flash_attention.default.tags
     assert torch.Tag.flexible_layout in torch.ops.xinfer.batched_flash_attention.default.tags
     shims = attention_c_shims()
-    assert len(shims) == 4
+    assert len(shims) == 5
     assert all(name in text[0] for name, text in zip(
         ("aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
-         "aoti_torch_cuda_append_kv_batched", "aoti_torch_cuda_qk_norm_rope_append"), shims.values()))
+         "aoti_torch_cuda_append_kv_batched", "aoti_torch_cuda_qk_norm_rope_append",
+         "aoti_torch_cuda_batched_flash_attention_bthd"), shims.values()))
     with FakeTensorMode(allow_non_fake_inputs=True):
         q = torch.empty(2, 16, 3, 128, dtype=torch.bfloat16, device="cuda").transpose(1, 2).contiguous().transpose(1, 2)
         k = torch.empty(2, 8, 64, 128, dtype=torch.bfloat16, device="cuda")

@@ -10,6 +10,8 @@ which registers three operators in the `xinfer` namespace:
   over each request's populated KV prefix (HIP kernels for gfx950);
 * ``append_kv_batched`` -- the in-place KV-cache append, native instead of the
   reference's Triton op (compiler/common/kernels/kv_cache.py:45-72);
+* ``batched_flash_attention_bthd`` -- ``batched_flash_attention`` with its
+  output in [B,T,Hq,D] order (the adapter's reshape then needs no copy);
 * ``qk_norm_rope_append`` -- the step before the attention operator in one
   launch: q/k RMSNorm, rotary embedding and the KV append
   (compiler/qwen3/adapters/attention.py:44-51), see xinfer_amd/norm_rope.py.
@@ -33,6 +35,10 @@ APPEND_KV_C_SHIM = """AOTITorchError aoti_torch_cuda_append_kv_batched(
     AtenTensorHandle key, AtenTensorHandle value, AtenTensorHandle positions,
     AtenTensorHandle cu_query, AtenTensorHandle cache_key, AtenTensorHandle cache_value,
     AtenTensorHandle* unused_output)"""
+BATCHED_BTHD_C_SHIM = """AOTITorchError aoti_torch_cuda_batched_flash_attention_bthd(
+    AtenTensorHandle q, AtenTensorHandle k, AtenTensorHandle v,
+    AtenTensorHandle offsets, AtenTensorHandle cuda_offsets, AtenTensorHandle blocks,
+    double scale, AtenTensorHandle* output)"""
 NORM_ROPE_C_SHIM = """AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
     AtenTensorHandle q, AtenTensorHandle key, AtenTensorHandle value,
     AtenTensorHandle q_weight, AtenTensorHandle k_weight, double eps,
@@ -139,6 +145,13 @@ def load_attention_ops(library=None, *, model=None):
             torch._check(blocks.shape == (q.shape[0], 1) and blocks.device == q.device)
             return fake(q, k, v, torch.empty(2, dtype=torch.uint8), scale)
 
+    if hasattr(torch.ops.xinfer, "batched_flash_attention_bthd"):
+
+        @torch.library.register_fake("xinfer::batched_flash_attention_bthd")
+        def fake_batched_bthd(q, k, v, offsets, cuda_offsets, blocks, scale):
+            out = fake_batched(q, k, v, offsets, cuda_offsets, blocks, scale)
+            return out.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
+
     if hasattr(torch.ops.xinfer, "append_kv_batched"):
 
         @torch.library.register_fake("xinfer::append_kv_batched")
@@ -174,7 +187,7 @@ def attention_c_shims():
 
     The reference maps the two attention operators (attention.py:105-112); the
     native append needs its own entry because it is no longer a Triton op, and
-    so does the fused norm/rope/append step.
+    so do the fused norm/rope/append step and the [B,T,Hq,D]-output variant.
     """
     import torch
 
@@ -183,4 +196,5 @@ def attention_c_shims():
         torch.ops.xinfer.batched_flash_attention.default: [BATCHED_ATTENTION_C_SHIM],
         torch.ops.xinfer.append_kv_batched.default: [APPEND_KV_C_SHIM],
         torch.ops.xinfer.qk_norm_rope_append.default: [NORM_ROPE_C_SHIM],
+        torch.ops.xinfer.batched_flash_attention_bthd.default: [BATCHED_BTHD_C_SHIM],
     }

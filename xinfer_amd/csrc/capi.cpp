@@ -260,7 +260,7 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
 }
 
 int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const xinfer_view4 &k,
-             const xinfer_view4 &v, double scale, void *out, void *workspace, hipStream_t stream) {
+             const xinfer_view4 &v, double scale, const xinfer_view4 &out, void *workspace, hipStream_t stream) {
   const int G = (int)(g.Hq / g.Hkv);
   const int dp = padded_dim(g.D);
   float *part_o = static_cast<float *>(workspace);
@@ -272,10 +272,10 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
       a->q = view_of(q);
       a->k = view_of(k);
       a->v = view_of(v);
-      a->out = static_cast<uint16_t *>(out);
-      a->o_sb = g.Hq * g.T * g.D;
-      a->o_sh = g.T * g.D;
-      a->o_st = g.D;
+      a->out = static_cast<uint16_t *>(const_cast<void *>(out.data));
+      a->o_sb = out.stride[0];
+      a->o_sh = out.stride[1];
+      a->o_st = out.stride[2];
       a->part_o = part_o;
       a->part_ml = part_ml;
       a->scale_log2 = (float)(scale * 1.4426950408889634);
@@ -294,10 +294,10 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
     }
     if (grp.merge_items > 0) {
       MergeArgs &m = grp.merge;
-      m.out = static_cast<uint16_t *>(out);
-      m.o_sb = g.Hq * g.T * g.D;
-      m.o_sh = g.T * g.D;
-      m.o_st = g.D;
+      m.out = static_cast<uint16_t *>(const_cast<void *>(out.data));
+      m.o_sb = out.stride[0];
+      m.o_sh = out.stride[1];
+      m.o_st = out.stride[2];
       m.part_o = part_o;
       m.part_ml = part_ml;
       m.D = (int32_t)g.D;
@@ -306,6 +306,32 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
       if (launch_merge(m, dp, grp.merge_max_splits, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
     }
   }
+  return XINFER_OK;
+}
+
+// The contiguous [B, Hq, T, D] output the operators allocate.
+xinfer_view4 contiguous_output(const Geometry &g, void *out) {
+  xinfer_view4 o{};
+  o.data = out;
+  const int64_t sizes[4] = {g.B, g.Hq, g.T, g.D};
+  const int64_t strides[4] = {g.Hq * g.T * g.D, g.T * g.D, g.D, 1};
+  for (int i = 0; i < 4; ++i) {
+    o.size[i] = sizes[i];
+    o.stride[i] = strides[i];
+  }
+  return o;
+}
+
+// An output view the kernels can write: q's sizes, unit feature stride, the
+// other strides multiples of 8 elements, 16-byte aligned data.
+int check_output(const Geometry &g, const xinfer_view4 *out) {
+  if (out == nullptr || out->data == nullptr) return XINFER_ERR_ARGUMENT;
+  const int64_t sizes[4] = {g.B, g.Hq, g.T, g.D};
+  for (int i = 0; i < 4; ++i)
+    if (out->size[i] != sizes[i]) return XINFER_ERR_QKV_SHAPES;
+  if ((reinterpret_cast<uintptr_t>(out->data) & 15u) != 0 || out->stride[3] != 1) return XINFER_ERR_LAYOUT;
+  for (int i = 0; i < 3; ++i)
+    if (out->stride[i] % 8 != 0 || out->stride[i] < 0) return XINFER_ERR_LAYOUT;
   return XINFER_OK;
 }
 
@@ -412,7 +438,23 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
   const Plan plan = make_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
-  return run_plan(plan, g, *q, *k, *v, scale, out, workspace, static_cast<hipStream_t>(stream));
+  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
+                  static_cast<hipStream_t>(stream));
+}
+
+int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                                       const int32_t *host_offsets, double scale, const xinfer_view4 *out,
+                                       void *workspace, size_t workspace_bytes, void *stream) {
+  Geometry g;
+  std::vector<int32_t> counts, lengths;
+  if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
+  if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (g.B == 0 || g.T == 0) return XINFER_OK;
+  if (int rc = check_output(g, out)) return rc;
+  const Plan plan = make_plan(g, counts, lengths);
+  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
+    return XINFER_ERR_WORKSPACE;
+  return run_plan(plan, g, *q, *k, *v, scale, *out, workspace, static_cast<hipStream_t>(stream));
 }
 
 size_t xinfer_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
@@ -434,7 +476,8 @@ int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const x
   const Plan plan = make_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
-  return run_plan(plan, g, *q, *k, *v, scale, out, workspace, static_cast<hipStream_t>(stream));
+  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
+                  static_cast<hipStream_t>(stream));
 }
 
 int xinfer_append_kv_batched(const xinfer_view4 *key, const xinfer_view4 *value,

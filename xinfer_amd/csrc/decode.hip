@@ -93,11 +93,13 @@ struct DecodeRegs {
 
 // Zero out[b, h*G + g, t, :] for g < G and t in [t_begin, T).
 __device__ __forceinline__ void zero_queries(const DecodeParams &a, int b, int h, int t_begin) {
-  const int per_head = (a.T - t_begin) * a.D / 8;  // 16-byte chunks per head
+  const int chunks = a.D / 8;                       // 16-byte chunks per query row
+  const int per_head = (a.T - t_begin) * chunks;
   for (int idx = threadIdx.x; idx < a.G * per_head; idx += blockDim.x) {
     const int g = idx / per_head, rest = idx - g * per_head;
-    uint16_t *dst = a.out + b * a.o_sb + (int64_t)(h * a.G + g) * a.o_sh + (int64_t)t_begin * a.o_st;
-    store16(dst + rest * 8, u32x4{0, 0, 0, 0});
+    const int t = t_begin + rest / chunks, c = rest - (rest / chunks) * chunks;
+    store16(a.out + b * a.o_sb + (int64_t)(h * a.G + g) * a.o_sh + (int64_t)t * a.o_st + c * 8,
+            u32x4{0, 0, 0, 0});
   }
 }
 

@@ -29,8 +29,8 @@ struct View {
 
 struct AttnArgs {
   View q, k, v;
-  uint16_t *out;             // contiguous [B, Hq, T, D]
-  int64_t o_sb, o_sh, o_st;  // = Hq*T*D, T*D, D
+  uint16_t *out;             // [B, Hq, T, D]: unit feature stride, other strides multiples of 8
+  int64_t o_sb, o_sh, o_st;  // contiguous: Hq*T*D, T*D, D; [B, T, Hq, D] storage: T*Hq*D, D, Hq*D
   float *part_o;             // [records][D] unnormalised fp32 partial outputs
   float *part_ml;            // [records][2] (running max in log2 units, sum)
   float scale_log2;          // softmax scale * log2(e)

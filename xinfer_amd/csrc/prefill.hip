@@ -202,10 +202,11 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int qrows = cnt * G, p0 = L - cnt;
 
   if (tile == 0 && split == 0 && cnt < T) {  // zero the row's padded queries
-    const int per = (T - cnt) * D / 8;
+    const int chunks = D / 8, per = (T - cnt) * chunks;
     for (int idx = tid; idx < G * per; idx += THREADS) {
       const int g = idx / per, rest = idx - g * per;
-      store16(a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)cnt * a.o_st + rest * 8,
+      const int t = cnt + rest / chunks, ch = rest - (rest / chunks) * chunks;
+      store16(a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)t * a.o_st + ch * 8,
               u32x4{0, 0, 0, 0});
     }
   }

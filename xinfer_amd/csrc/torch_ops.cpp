@@ -58,10 +58,11 @@ void check_status(int status) { TORCH_CHECK(status == XINFER_OK, xinfer_status_s
 
 }  // namespace
 
-// Replaces compiler/common/kernels/attention.cpp:14-79.
-at::Tensor batched_flash_attention(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
-                                   const at::Tensor &offsets, const at::Tensor &cuda_offsets,
-                                   const at::Tensor &blocks, double scale) {
+// Replaces compiler/common/kernels/attention.cpp:14-79.  With `bthd` the
+// output is a contiguous [B,T,Hq,D] tensor instead (the optional variant).
+at::Tensor batched_attention(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
+                             const at::Tensor &offsets, const at::Tensor &cuda_offsets, const at::Tensor &blocks,
+                             double scale, bool bthd) {
   TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.sizes() == k.sizes() && k.size(0) == q.size(0) &&
                   k.size(3) == q.size(3),
               "Invalid Q/K/V shapes");
@@ -90,7 +91,8 @@ at::Tensor batched_flash_attention(const at::Tensor &q, const at::Tensor &k, con
     max_length = std::max(max_length, length);
   }
   c10::DeviceGuard guard(q.device());
-  auto output = at::empty(q.sizes(), q.options());
+  auto output = bthd ? at::empty({q.size(0), q.size(2), q.size(1), q.size(3)}, q.options())
+                     : at::empty(q.sizes(), q.options());
   if (batch == 0 || q.size(2) == 0) return output;
   // Row r's KV lives in k[r]/v[r]: `blocks` is the identity page table built by
   // batched_attention_metadata and needs no read.  Copy only what the kernels
@@ -106,9 +108,30 @@ at::Tensor batched_flash_attention(const at::Tensor &q, const at::Tensor &k, con
   auto qv = view_of(query), kv = view_of(key), vv = view_of(value);
   const size_t bytes = xinfer_batched_flash_attention_workspace_size(&qv, &kv, cuq);
   auto workspace = at::empty({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
-  check_status(xinfer_batched_flash_attention(&qv, &kv, &vv, cuq, scale, output.data_ptr(),
-                                              workspace.data_ptr(), bytes, current_stream(q)));
+  if (bthd) {
+    auto ov = view_of(output.transpose(1, 2));
+    check_status(xinfer_batched_flash_attention_out(&qv, &kv, &vv, cuq, scale, &ov, workspace.data_ptr(), bytes,
+                                                    current_stream(q)));
+  } else {
+    check_status(xinfer_batched_flash_attention(&qv, &kv, &vv, cuq, scale, output.data_ptr(),
+                                                workspace.data_ptr(), bytes, current_stream(q)));
+  }
   return output;
+}
+
+at::Tensor batched_flash_attention(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
+                                   const at::Tensor &offsets, const at::Tensor &cuda_offsets,
+                                   const at::Tensor &blocks, double scale) {
+  return batched_attention(q, k, v, offsets, cuda_offsets, blocks, scale, false);
+}
+
+// The optional variant of compiler/qwen3/adapters/attention.py:58-61: the same
+// operation with the output already in the [B,T,Hq,D] order the adapter
+// reshapes to [B,T,Hq*D], so that reshape is a view instead of a copy.
+at::Tensor batched_flash_attention_bthd(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
+                                        const at::Tensor &offsets, const at::Tensor &cuda_offsets,
+                                        const at::Tensor &blocks, double scale) {
+  return batched_attention(q, k, v, offsets, cuda_offsets, blocks, scale, true);
 }
 
 // Replaces compiler/common/kernels/attention.cpp:82-124.
@@ -238,6 +261,9 @@ TORCH_LIBRARY(xinfer, m) {
         {at::Tag::flexible_layout});
   m.def("flash_attention(Tensor q, Tensor k, Tensor v, Tensor kv_extent, float scale) -> Tensor",
         {at::Tag::flexible_layout});
+  m.def("batched_flash_attention_bthd(Tensor q, Tensor k, Tensor v, Tensor offsets, "
+        "Tensor cuda_offsets, Tensor blocks, float scale) -> Tensor",
+        {at::Tag::flexible_layout});
   m.def("append_kv_batched(Tensor key, Tensor value, Tensor positions, Tensor cu_query, "
         "Tensor(a4!) cache_key, Tensor(a5!) cache_value) -> ()");
   m.def("qk_norm_rope_append(Tensor q, Tensor key, Tensor value, Tensor q_weight, Tensor k_weight, "
@@ -248,6 +274,7 @@ TORCH_LIBRARY(xinfer, m) {
 TORCH_LIBRARY_IMPL(xinfer, CUDA, m) {
   m.impl("batched_flash_attention", TORCH_FN(xinfer::batched_flash_attention));
   m.impl("flash_attention", TORCH_FN(xinfer::flash_attention));
+  m.impl("batched_flash_attention_bthd", TORCH_FN(xinfer::batched_flash_attention_bthd));
   m.impl("append_kv_batched", TORCH_FN(xinfer::append_kv_batched));
   m.impl("qk_norm_rope_append", TORCH_FN(xinfer::qk_norm_rope_append));
 }
@@ -262,6 +289,17 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_batched_flash_attention(
     AtenTensorHandle cuda_offsets, AtenTensorHandle blocks, double scale, AtenTensorHandle *output) {
   AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
     *output = new_tensor_handle(xinfer::batched_flash_attention(
+        resolve_tensor_dispatch_flags(q), resolve_tensor_dispatch_flags(k),
+        resolve_tensor_dispatch_flags(v), resolve_tensor_dispatch_flags(offsets),
+        resolve_tensor_dispatch_flags(cuda_offsets), resolve_tensor_dispatch_flags(blocks), scale));
+  });
+}
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_batched_flash_attention_bthd(
+    AtenTensorHandle q, AtenTensorHandle k, AtenTensorHandle v, AtenTensorHandle offsets,
+    AtenTensorHandle cuda_offsets, AtenTensorHandle blocks, double scale, AtenTensorHandle *output) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    *output = new_tensor_handle(xinfer::batched_flash_attention_bthd(
         resolve_tensor_dispatch_flags(q), resolve_tensor_dispatch_flags(k),
         resolve_tensor_dispatch_flags(v), resolve_tensor_dispatch_flags(offsets),
         resolve_tensor_dispatch_flags(cuda_offsets), resolve_tensor_dispatch_flags(blocks), scale));
