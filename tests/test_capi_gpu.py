@@ -150,8 +150,9 @@ def test_split_merge_survives_garbage_and_reused_workspace(capi, gpu_ops):
 
 @torch.inference_mode()
 def test_split_merge_in_graph_replays(gpu_ops):
-    """A captured call replays with the same arrival counters: every replay,
-    on new inputs copied into the captured buffers, matches an eager call."""
+    """A captured call with split records and a merge launch replays exactly:
+    every replay, on new inputs copied into the captured buffers, matches an
+    eager call bit for bit."""
     torch.manual_seed(80)
     batch, heads, kv_heads, dim, capacity = 2, 16, 8, 128, 8192
     counts, lengths = [1, 512], [8000, 2048]
@@ -174,3 +175,55 @@ def test_split_merge_in_graph_replays(gpu_ops):
         eager = gpu_ops.batched_flash_attention(q, k, v, host, cu, blocks, dim**-0.5)
         torch.cuda.synchronize()
         assert torch.equal(captured.view(torch.int16), eager.view(torch.int16)), replay
+
+
+@torch.inference_mode()
+def test_fused_step_in_graph_replays(gpu_ops):
+    """The serving step with the optional operators -- fused norm/rope/append,
+    then attention with [B,T,Hq,D] output -- captured once and replayed on new
+    projections: every replay matches an eager step bit for bit (output and
+    both caches), with eager work in between.  The per-step metadata is built
+    before capture, as a serving loop keeps it in persistent buffers."""
+    from xinfer_amd.norm_rope import qk_norm_rope_append
+
+    torch.manual_seed(81)
+    batch, tokens, heads, kv_heads, dim, capacity = 4, 1, 16, 8, 128, 4096
+    prefixes = [3000, 17, 900, 4000]
+    counts = [1, 1, 0, 1]
+    lengths = [p + c for p, c in zip(prefixes, counts)]
+    options = dict(device="cuda", dtype=torch.bfloat16)
+    q = torch.randn(batch, tokens, heads, dim, **options)
+    k = torch.randn(batch, tokens, kv_heads, dim, **options)
+    v = torch.randn_like(k)
+    weights = [1 + 0.1 * torch.randn(dim, **options) for _ in range(2)]
+    angle = torch.rand(batch, tokens, dim, device="cuda")
+    cos, sin = angle.cos().to(torch.bfloat16), angle.sin().to(torch.bfloat16)
+    positions = torch.tensor(prefixes, device="cuda")[:, None]
+    caches = [torch.randn(batch, kv_heads, capacity, dim, **options) for _ in range(2)]
+    base = [c.clone() for c in caches]
+    host, cu, blocks = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
+
+    def step():
+        qr = qk_norm_rope_append(q, k, v, weights[0], weights[1], 1e-6, cos, sin, positions, cu[0], *caches)
+        return gpu_ops.batched_flash_attention_bthd(qr, caches[0], caches[1], host, cu, blocks, dim**-0.5)
+
+    step()  # warm-up outside capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = step()
+    for replay in range(3):
+        for c, b in zip(caches, base):
+            c.copy_(b)
+        q.copy_(torch.randn_like(q))
+        k.copy_(torch.randn_like(k))
+        graph.replay()
+        torch.cuda.synchronize()
+        replayed = [captured.clone()] + [c.clone() for c in caches]
+        for c, b in zip(caches, base):
+            c.copy_(b)
+        eager = step()
+        torch.cuda.synchronize()
+        assert torch.equal(replayed[0].view(torch.int16), eager.view(torch.int16)), replay
+        assert all(torch.equal(a, b) for a, b in zip(replayed[1:], caches)), replay

@@ -83,6 +83,11 @@ def batched_attention_metadata(kv_lengths, query_lengths, device):
         (torch.zeros((2, 1), dtype=torch.int32), lengths.cumsum(1, dtype=torch.int32)), dim=1
     )
     blocks = torch.arange(kv_lengths.shape[0], device=device, dtype=torch.int32)[:, None]
+    if torch.device(device).type == "cuda":
+        # Pinned source: the copy is queued on the current stream without
+        # blocking the host, and is a capturable graph node.
+        offsets = offsets.pin_memory()
+        return offsets, offsets.to(device, non_blocking=True), blocks
     return offsets, offsets.to(device), blocks
 
 
