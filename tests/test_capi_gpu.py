@@ -115,9 +115,10 @@ def test_flash_and_append_through_c_abi(capi, gpu_ops):
 
 @torch.inference_mode()
 def test_split_merge_survives_garbage_and_reused_workspace(capi, gpu_ops):
-    """Split rows merge inside the attention launch through arrival counters in
-    the workspace.  A workspace full of arbitrary bytes, then the same workspace
-    reused by later calls on other inputs, must still give the torch results."""
+    """Split rows write partial records into the caller's workspace and a
+    merge launch folds them.  A workspace full of arbitrary bytes, then the
+    same workspace reused by later calls on other inputs, must still give the
+    torch results: no record is read before it is written."""
     torch.manual_seed(79)
     batch, heads, kv_heads, dim, capacity = 3, 16, 8, 128, 16384
     counts, lengths = [1, 200, 1], [13000, 5000, 3000]
