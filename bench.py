@@ -23,8 +23,8 @@ attention operator alone, and divides the algorithmic work (KV bytes for
 decode, causal FLOPs for prefill) by that average duration.
 
 The CPU baseline times the numpy oracle (fp32) on the host cores over a
-bounded sample of the same workload, and, as BASELINE.md plans, torch's CPU
-SDPA on bf16 tensors (the reference CPU path), both with thread counts.
+bounded sample of the same workload, and torch's CPU SDPA on bf16 tensors
+(the reference CPU path), both with thread counts.
 """
 
 from __future__ import annotations
@@ -522,7 +522,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}). "
-              "The attention operator would shard by rows or KV heads with no exchange; see DESIGN.md.",
+              "The attention operator would shard by rows or KV heads with no exchange.",
               file=sys.stderr)
         sys.exit(2)
     import torch
