@@ -91,7 +91,8 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
 /* Same operation with the output written through a caller-supplied view of
  * q's sizes [B,Hq,T,D] (unit feature stride, other strides multiples of 8,
  * 16-byte aligned data), e.g. [B,T,Hq,D] storage viewed as [B,Hq,T,D].  The
- * workspace is the one *_workspace_size reports.  No reference counterpart:
+ * view's elements must be distinct and must not overlap q, k, v or the
+ * workspace.  The workspace is the one *_workspace_size reports.  No reference counterpart:
  * it serves xinfer::batched_flash_attention_bthd, the optional variant that
  * spares compiler/qwen3/adapters/attention.py:61 its transpose copy. */
 int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4 *k,
