@@ -1,6 +1,6 @@
 """Benchmark of the xinfer attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--norm-rope] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--norm-rope] [--gemv] [--no-cpu-baseline]
 
 A step is one pass of the hot path over one batch: the in-place KV append of
 each row's new tokens followed by one attention call over the populated
@@ -474,6 +474,57 @@ def measure_norm_rope(index, seed, iters=200):
     return result
 
 
+GEMV_SHAPES = ((8224, 1024), (1024, 2048), (7168, 1024), (1024, 3584), (5120, 1024))
+
+
+def measure_gemv(replays=20, per_graph=50):
+    """xinfer::projection_gemv on the reference's profiled decoder geometries
+    (compiler/common/passes/projection_gemv.py: PROFILED_SHAPES), bf16, against
+    torch's F.linear on the same operands.  Both are captured in HIP graphs of
+    `per_graph` calls over 8 weight copies (so consecutive calls do not find
+    their weight in the Infinity Cache) and timed with HIP events; bytes are
+    the weight's n*k*2 read once per call."""
+    import torch
+    from xinfer_amd.projection_gemv import projection_gemv
+
+    results = []
+    for n, k in GEMV_SHAPES:
+        copies = max(2, min(8, (MALL_BYTES * 2) // (n * k * 2) + 1))
+        weights = [torch.randn(n, k, device="cuda").div_(k**0.5).to(torch.bfloat16) for _ in range(copies)]
+        x = torch.randn(1, k, device="cuda").to(torch.bfloat16)
+
+        def per_call_us(function):
+            with torch.inference_mode():
+                for i in range(copies):
+                    function(x, weights[i])
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for i in range(per_graph):
+                        function(x, weights[i % copies])
+                graph.replay()
+                start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                torch.cuda.synchronize()
+                start.record()
+                for _ in range(replays):
+                    graph.replay()
+                end.record()
+                end.synchronize()
+            return start.elapsed_time(end) * 1e3 / (replays * per_graph)
+
+        ours = per_call_us(projection_gemv)
+        linear = per_call_us(torch.nn.functional.linear)
+        moved = n * k * 2
+        results.append({"n": n, "k": k, "us": round(ours, 2), "GBs": round(moved / ours / 1e3, 1),
+                        "frac_hbm": round(moved / ours / 1e3 / HBM_PEAK_GBS, 4),
+                        "torch_linear_us": round(linear, 2)})
+        log(f"[bench] projection gemv n={n} k={k}: {ours:.2f} us = {moved / ours / 1e3:.1f} GB/s; "
+            f"F.linear {linear:.2f} us")
+        del weights
+        torch.cuda.empty_cache()
+    return results
+
+
 COPY_PROBE_BYTES = 256 << 20
 
 
@@ -507,6 +558,8 @@ def main():
     parser.add_argument("--norm-rope", action="store_true",
                         help="only time the fused norm/rope/append step against the eager modules and print "
                              "its JSON (cfg2 and cfg3 token shapes)")
+    parser.add_argument("--gemv", action="store_true",
+                        help="only time xinfer::projection_gemv against F.linear on the decoder geometries")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
@@ -539,6 +592,9 @@ def main():
         copy_probe()
     if args.norm_rope:
         print(json.dumps({"norm_rope": [measure_norm_rope(2, 0), measure_norm_rope(3, 0)]}), flush=True)
+        return
+    if args.gemv:
+        print(json.dumps({"projection_gemv": measure_gemv()}), flush=True)
         return
     with_cpu = not args.no_cpu_baseline
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
@@ -584,6 +640,7 @@ def main():
         log(f"[bench] cfg3 seeds 0-7 aggregate: {moved} B in {op_us:.1f} us = {moved / op_us / 1e3:.1f} GB/s")
     if args.all:
         line["norm_rope"] = [measure_norm_rope(2, 0), measure_norm_rope(3, 0)]
+        line["projection_gemv"] = measure_gemv()
     print(json.dumps(line), flush=True)
 
 

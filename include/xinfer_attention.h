@@ -142,6 +142,19 @@ int xinfer_qk_norm_rope_append(const xinfer_view4 *q, const xinfer_view4 *key, c
                                void *q_out, const xinfer_view4 *cache_key, const xinfer_view4 *cache_value,
                                void *stream);
 
+/* ---------------------------------------------------------------------------
+ * xinfer::projection_gemv -- replaces the Triton op
+ * compiler/common/kernels/projection_gemv.py:10-62 (the decoder's singleton
+ * projections, selected by compiler/common/passes/projection_gemv.py).
+ *
+ * out[i] = sum_j weight[i, j] * x[j] for i < n, j < k: x [k] contiguous,
+ * weight [n, k] contiguous row-major, out [n]; all XINFER_BF16 or all
+ * XINFER_FP32 (dtype), accumulated in fp32.  out must not overlap x or weight.
+ * ------------------------------------------------------------------------- */
+enum { XINFER_BF16 = 0, XINFER_FP32 = 1 };
+int xinfer_projection_gemv(const void *x, const void *weight, void *out, int64_t n, int64_t k, int dtype,
+                           void *stream);
+
 /* The AOTInductor C shims of the same library are declared in
  * xinfer_attention_aoti.h. */
 

@@ -69,6 +69,12 @@ AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
     AtenTensorHandle positions, AtenTensorHandle cu_query, AtenTensorHandle cache_key,
     AtenTensorHandle cache_value, AtenTensorHandle *output);
 
+/* New: the native xinfer::projection_gemv (replaces the Triton op
+ * compiler/common/kernels/projection_gemv.py:35-62, which AOTI compiled into
+ * the wrapper).  Returns the new [*x.shape[:-1], n] output. */
+AOTITorchError aoti_torch_cuda_projection_gemv(AtenTensorHandle x, AtenTensorHandle weight,
+                                               AtenTensorHandle *output);
+
 #ifdef __cplusplus
 }
 #endif

@@ -70,7 +70,8 @@ def lib(library_path):
 def test_every_declared_symbol_is_exported(lib):
     names = declared_functions()
     assert {"xinfer_flash_attention", "xinfer_batched_flash_attention", "xinfer_append_kv_batched",
-            "xinfer_qk_norm_rope_append", "xinfer_batched_flash_attention_out", "aoti_torch_cuda_flash_attention",
+            "xinfer_qk_norm_rope_append", "xinfer_batched_flash_attention_out", "xinfer_projection_gemv",
+            "aoti_torch_cuda_projection_gemv", "aoti_torch_cuda_flash_attention",
             "aoti_torch_cuda_batched_flash_attention", "aoti_torch_cuda_append_kv_batched",
             "aoti_torch_cuda_qk_norm_rope_append"} <= set(names)
     for name in names:
@@ -164,6 +165,17 @@ def test_output_view_validation_codes(lib):
     assert call(ctypes.byref(view([2, 16, 4, 128], [4 * 16 * 256, 256, 16 * 256, 2]))) == 11
 
 
+def test_projection_gemv_validation_codes(lib):
+    """Rejected arguments return before any launch."""
+    call = lambda x, w, out, n, k, dtype: lib.xinfer_projection_gemv(  # noqa: E731
+        ctypes.c_void_p(x), ctypes.c_void_p(w), ctypes.c_void_p(out), ctypes.c_int64(n), ctypes.c_int64(k),
+        ctypes.c_int(dtype), None)
+    assert call(0, 1 << 20, 1 << 21, 4, 8, 0) == 14
+    assert call(1 << 20, 1 << 20, 1 << 21, 0, 8, 0) == 14
+    assert call(1 << 20, 1 << 20, 1 << 21, 4, -1, 1) == 14
+    assert call(1 << 20, 1 << 20, 1 << 21, 4, 8, 2) == 14
+
+
 def test_workspace_size_is_a_pure_host_query(lib):
     q, k = view([8, 16, 1, 128]), view([8, 8, 16384, 128])
     lengths = [13312, 2162, 386, 9459, 1399, 3852, 55, 182]
@@ -217,11 +229,11 @@ def test_operator_schemas_tags_and_fakes(library_path):
     assert torch.Tag.flexible_layout in torch.ops.xinfer.flash_attention.default.tags
     assert torch.Tag.flexible_layout in torch.ops.xinfer.batched_flash_attention.default.tags
     shims = attention_c_shims()
-    assert len(shims) == 5
+    assert len(shims) == 6
     assert all(name in text[0] for name, text in zip(
         ("aoti_torch_cuda_flash_attention", "aoti_torch_cuda_batched_flash_attention",
          "aoti_torch_cuda_append_kv_batched", "aoti_torch_cuda_qk_norm_rope_append",
-         "aoti_torch_cuda_batched_flash_attention_bthd"), shims.values()))
+         "aoti_torch_cuda_batched_flash_attention_bthd", "aoti_torch_cuda_projection_gemv"), shims.values()))
     with FakeTensorMode(allow_non_fake_inputs=True):
         q = torch.empty(2, 16, 3, 128, dtype=torch.bfloat16, device="cuda").transpose(1, 2).contiguous().transpose(1, 2)
         k = torch.empty(2, 8, 64, 128, dtype=torch.bfloat16, device="cuda")

@@ -12,6 +12,8 @@ which registers three operators in the `xinfer` namespace:
   reference's Triton op (compiler/common/kernels/kv_cache.py:45-72);
 * ``batched_flash_attention_bthd`` -- ``batched_flash_attention`` with its
   output in [B,T,Hq,D] order (the adapter's reshape then needs no copy);
+* ``projection_gemv`` -- the decoder's singleton projections, native instead
+  of the reference's Triton op (compiler/common/kernels/projection_gemv.py);
 * ``qk_norm_rope_append`` -- the step before the attention operator in one
   launch: q/k RMSNorm, rotary embedding and the KV append
   (compiler/qwen3/adapters/attention.py:44-51), see xinfer_amd/norm_rope.py.
@@ -39,6 +41,8 @@ BATCHED_BTHD_C_SHIM = """AOTITorchError aoti_torch_cuda_batched_flash_attention_
     AtenTensorHandle q, AtenTensorHandle k, AtenTensorHandle v,
     AtenTensorHandle offsets, AtenTensorHandle cuda_offsets, AtenTensorHandle blocks,
     double scale, AtenTensorHandle* output)"""
+PROJECTION_GEMV_C_SHIM = """AOTITorchError aoti_torch_cuda_projection_gemv(
+    AtenTensorHandle x, AtenTensorHandle weight, AtenTensorHandle* output)"""
 NORM_ROPE_C_SHIM = """AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
     AtenTensorHandle q, AtenTensorHandle key, AtenTensorHandle value,
     AtenTensorHandle q_weight, AtenTensorHandle k_weight, double eps,
@@ -165,6 +169,13 @@ def load_attention_ops(library=None, *, model=None):
             torch._check(cache_key.is_contiguous() and cache_value.is_contiguous())
             return None
 
+    if hasattr(torch.ops.xinfer, "projection_gemv"):
+
+        @torch.library.register_fake("xinfer::projection_gemv")
+        def fake_projection(x, weight):
+            torch._check(weight.dim() == 2 and x.dim() >= 2 and x.shape[-1] == weight.shape[1])
+            return x.new_empty((*x.shape[:-1], weight.shape[0]))
+
     if hasattr(torch.ops.xinfer, "qk_norm_rope_append"):
 
         @torch.library.register_fake("xinfer::qk_norm_rope_append")
@@ -192,7 +203,8 @@ def attention_c_shims():
 
     The reference maps the two attention operators (attention.py:105-112); the
     native append needs its own entry because it is no longer a Triton op, and
-    so do the fused norm/rope/append step and the [B,T,Hq,D]-output variant.
+    so do the fused norm/rope/append step, the [B,T,Hq,D]-output variant and
+    the native projection GEMV (a Triton op in the reference).
     """
     import torch
 
@@ -202,4 +214,5 @@ def attention_c_shims():
         torch.ops.xinfer.append_kv_batched.default: [APPEND_KV_C_SHIM],
         torch.ops.xinfer.qk_norm_rope_append.default: [NORM_ROPE_C_SHIM],
         torch.ops.xinfer.batched_flash_attention_bthd.default: [BATCHED_BTHD_C_SHIM],
+        torch.ops.xinfer.projection_gemv.default: [PROJECTION_GEMV_C_SHIM],
     }

@@ -592,4 +592,18 @@ int xinfer_qk_norm_rope_append(const xinfer_view4 *q, const xinfer_view4 *key, c
   return launch_norm_rope(a, static_cast<hipStream_t>(stream)) == hipSuccess ? XINFER_OK : XINFER_ERR_LAUNCH;
 }
 
+int xinfer_projection_gemv(const void *x, const void *weight, void *out, int64_t n, int64_t k, int dtype,
+                           void *stream) {
+  if (!x || !weight || !out || n <= 0 || k <= 0 || k >= (int64_t(1) << 31) || n >= (int64_t(1) << 31) ||
+      (dtype != XINFER_BF16 && dtype != XINFER_FP32))
+    return XINFER_ERR_ARGUMENT;
+  const int64_t size = dtype == XINFER_FP32 ? 4 : 2;
+  const bool vec = (reinterpret_cast<uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<uintptr_t>(weight) & 15u) == 0 &&
+                   (k * size) % 16 == 0;
+  GemvArgs a{x, weight, out, n, k};
+  return launch_gemv(a, dtype == XINFER_FP32, vec, static_cast<hipStream_t>(stream)) == hipSuccess
+             ? XINFER_OK
+             : XINFER_ERR_LAUNCH;
+}
+
 }  // extern "C"

@@ -91,4 +91,12 @@ struct NormRopeArgs {
   int32_t B, T, Hq, Hkv, D, C;
 };
 
+// Singleton projection (gemv.hip).
+struct GemvArgs {
+  const void *x;       // [k]
+  const void *weight;  // [n, k] row-major
+  void *out;           // [n]
+  int64_t n, k;
+};
+
 }  // namespace xattn

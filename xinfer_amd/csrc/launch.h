@@ -9,6 +9,8 @@ namespace xattn {
 
 hipError_t launch_append(const AppendArgs &a, bool vector, hipStream_t stream);
 hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t stream);
+// fp32: float inputs and output, else bf16; vec: 16-byte aligned rows and input.
+hipError_t launch_gemv(const GemvArgs &a, bool fp32, bool vec, hipStream_t stream);
 
 // Keys handled by one decode work item for padded head dim `dp` and `qr` query
 // vectors per KV head (a power of two <= 8).

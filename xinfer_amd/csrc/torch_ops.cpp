@@ -16,6 +16,7 @@
 #include <torch/library.h>
 
 #include <cmath>
+#include <vector>
 
 #include "xinfer_attention.h"
 #include "xinfer_attention_aoti.h"
@@ -253,6 +254,29 @@ at::Tensor qk_norm_rope_append(const at::Tensor &q, const at::Tensor &key, const
   return output;
 }
 
+// Replaces the Triton op compiler/common/kernels/projection_gemv.py:35-62,
+// with its checks, their order and messages (ValueError in Python).
+at::Tensor projection_gemv(const at::Tensor &x, const at::Tensor &weight) {
+  TORCH_CHECK_VALUE(x.is_cuda() && weight.device() == x.device(), "Projection GEMV requires colocated CUDA tensors");
+  TORCH_CHECK_VALUE((x.scalar_type() == at::kBFloat16 || x.scalar_type() == at::kFloat) &&
+                        weight.scalar_type() == x.scalar_type(),
+                    "Projection GEMV requires matching BF16 or FP32 tensors");
+  bool singleton = x.dim() >= 2 && weight.dim() == 2;
+  for (int64_t d = 0; singleton && d + 1 < x.dim(); ++d) singleton = x.size(d) == 1;
+  TORCH_CHECK_VALUE(singleton, "Projection GEMV requires one input row and a 2D weight");
+  TORCH_CHECK_VALUE(x.size(-1) == weight.size(1) && x.stride(-1) == 1 && weight.is_contiguous(),
+                    "Projection GEMV requires matching contiguous reduction dimensions");
+  const int64_t n = weight.size(0), k = weight.size(1);
+  TORCH_CHECK_VALUE(n > 0 && k > 0, "Projection GEMV requires positive dimensions");
+  c10::DeviceGuard guard(x.device());
+  std::vector<int64_t> shape(x.sizes().begin(), x.sizes().end());
+  shape.back() = n;
+  auto output = at::empty(shape, x.options());
+  check_status(xinfer_projection_gemv(x.data_ptr(), weight.data_ptr(), output.data_ptr(), n, k,
+                                      x.scalar_type() == at::kFloat ? XINFER_FP32 : XINFER_BF16, current_stream(x)));
+  return output;
+}
+
 }  // namespace xinfer
 
 TORCH_LIBRARY(xinfer, m) {
@@ -266,6 +290,7 @@ TORCH_LIBRARY(xinfer, m) {
         {at::Tag::flexible_layout});
   m.def("append_kv_batched(Tensor key, Tensor value, Tensor positions, Tensor cu_query, "
         "Tensor(a4!) cache_key, Tensor(a5!) cache_value) -> ()");
+  m.def("projection_gemv(Tensor x, Tensor weight) -> Tensor");
   m.def("qk_norm_rope_append(Tensor q, Tensor key, Tensor value, Tensor q_weight, Tensor k_weight, "
         "float eps, Tensor cos, Tensor sin, Tensor positions, Tensor cu_query, Tensor(a10!) cache_key, "
         "Tensor(a11!) cache_value) -> Tensor");
@@ -277,6 +302,7 @@ TORCH_LIBRARY_IMPL(xinfer, CUDA, m) {
   m.impl("batched_flash_attention_bthd", TORCH_FN(xinfer::batched_flash_attention_bthd));
   m.impl("append_kv_batched", TORCH_FN(xinfer::append_kv_batched));
   m.impl("qk_norm_rope_append", TORCH_FN(xinfer::qk_norm_rope_append));
+  m.impl("projection_gemv", TORCH_FN(xinfer::projection_gemv));
 }
 
 using torch::aot_inductor::new_tensor_handle;
@@ -339,6 +365,14 @@ AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_qk_norm_rope_append(
         resolve_tensor_dispatch_flags(cos), resolve_tensor_dispatch_flags(sin),
         resolve_tensor_dispatch_flags(positions), resolve_tensor_dispatch_flags(cu_query),
         resolve_tensor_dispatch_flags(cache_key), resolve_tensor_dispatch_flags(cache_value)));
+  });
+}
+
+AOTI_TORCH_EXPORT AOTITorchError aoti_torch_cuda_projection_gemv(AtenTensorHandle x, AtenTensorHandle weight,
+                                                                 AtenTensorHandle *output) {
+  AOTI_TORCH_CONVERT_EXCEPTION_TO_ERROR_CODE({
+    *output = new_tensor_handle(
+        xinfer::projection_gemv(resolve_tensor_dispatch_flags(x), resolve_tensor_dispatch_flags(weight)));
   });
 }
 
