@@ -35,6 +35,11 @@ CASES = {
     "prefill_4_2_128": (4, 2, 128, 200, [100], [180], "random"),
     "ragged_4_1_256": (4, 1, 256, 128, [40, 0, 3, 17], [90, 12, 3, 120], "random"),
     "geometry_6_2_64": (6, 2, 64, 160, [16], [129], "random"),
+    # Head dims that are not a padded kernel width (the contract is any
+    # multiple of 8 in 8..256): a prefill row and two decode rows at D = 72,
+    # and a prefill and a decode row with one query head per KV head at D = 136.
+    "odd_dim_4_2_72": (4, 2, 72, 160, [30, 1, 2], [120, 77, 2], "random"),
+    "odd_dim_3_3_136": (3, 3, 136, 200, [12, 1], [150, 190], "random"),
 }
 APPEND_CASE = dict(batch=3, heads=2, tokens=6, dim=64, capacity=40, counts=[6, 0, 2])
 

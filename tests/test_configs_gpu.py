@@ -1,12 +1,18 @@
 """Parity of one hot-path step (KV append + attention) on the five measured configurations.
 
 Inputs are the seeded CPU draws of xinfer_amd.workloads (identical bits for the
-GPU and the CPU oracle).  Gates: the KV caches after the append
-are bit-identical to the oracle append; attention outputs are within max-abs
-2e-2 and mean-abs 2e-3 of the float64 oracle; and the error is no worse than
-the reference path's own bf16 error -- torch SDPA on bf16 tensors with the
-explicit lower-right mask (the adapted eager attention) on the device's
-flash-family kernels, measured on the same inputs -- within BF16_SLACK.
+GPU and the CPU oracle).  Gates:
+
+* the KV caches after the append equal, bit for bit, the caches the workload
+  builds on the CPU by slice assignment of the new tokens (every untouched
+  slot included);
+* attention outputs are within max-abs 2e-2 and mean-abs 2e-3 of the float64
+  oracle;
+* the error is no worse than the reference path's own bf16 error: torch SDPA
+  on bf16 tensors with the explicit lower-right mask (the adapted eager
+  attention) on the device's flash-family kernels, measured on the same rows
+  and inputs.  Both the worst and the mean absolute error must be at or below
+  the reference path's.
 """
 
 import numpy as np
@@ -23,9 +29,9 @@ from xinfer_amd.attention import batched_attention_metadata, cache_extent
 
 pytestmark = pytest.mark.gpu
 
-# Our error may exceed the bf16 reference path's error by at most this factor
-# (both are dominated by the final bf16 rounding of the output).
-BF16_SLACK = 1.25
+# Our error may exceed the bf16 reference path's error by at most this factor:
+# BASELINE.json asks for "no worse than the reference's own bf16 error".
+BF16_SLACK = 1.0
 
 
 def row_slices(inputs, r, length, count):
@@ -96,8 +102,9 @@ def test_config_parity(gpu_ops, index, seed):
         assert torch.equal(k_gpu.cpu().view(torch.int16), inputs["k_after"].view(torch.int16))
         assert torch.equal(v_gpu.cpu().view(torch.int16), inputs["v_after"].view(torch.int16))
     del k_gpu, v_gpu
-    worst = dict(max_abs=0.0, sum_abs=0.0, n=0, ref_max_abs=0.0, ref_sum_abs=0.0, ref_n=0)
-    reference_rows = range(w.batch) if index != 5 else range(0, w.batch, 4)
+    # Every row is compared three ways on the same elements: ours and the bf16
+    # reference path, each against the float64 oracle.
+    worst = dict(max_abs=0.0, sum_abs=0.0, n=0, ref_max_abs=0.0, ref_sum_abs=0.0)
     for r, (count, length) in enumerate(zip(w.counts, w.lengths)):
         assert torch.count_nonzero(out[r, :, count:]).item() == 0
         q, k, v = row_slices(inputs, r, length, count)
@@ -107,26 +114,20 @@ def test_config_parity(gpu_ops, index, seed):
         worst["max_abs"] = max(worst["max_abs"], float(delta.max()))
         worst["sum_abs"] += float(delta.sum())
         worst["n"] += delta.size
-        if r in reference_rows:
-            ref, source = bf16_reference(q, k, v, count, length, w.scale)
-            ref = ref.float().numpy().astype(np.float64)
-            worst["source"] = source
-            ref_delta = np.abs(ref - expected)
-            worst["ref_max_abs"] = max(worst["ref_max_abs"], float(ref_delta.max()))
-            worst["ref_sum_abs"] += float(ref_delta.sum())
-            worst["ref_n"] += ref_delta.size
-            ours_rows = np.abs(out[r : r + 1, :, :count].float().numpy().astype(np.float64) - expected)
-            worst.setdefault("ours_on_ref_rows", 0.0)
-            worst["ours_on_ref_rows"] += float(ours_rows.sum())
+        ref, source = bf16_reference(q, k, v, count, length, w.scale)
+        ref_delta = np.abs(ref.float().numpy().astype(np.float64) - expected)
+        worst["source"] = source
+        worst["ref_max_abs"] = max(worst["ref_max_abs"], float(ref_delta.max()))
+        worst["ref_sum_abs"] += float(ref_delta.sum())
     mean_abs = worst["sum_abs"] / worst["n"]
-    ref_mean = worst["ref_sum_abs"] / worst["ref_n"]
-    ours_mean_on_ref_rows = worst["ours_on_ref_rows"] / worst["ref_n"]
+    ref_mean = worst["ref_sum_abs"] / worst["n"]
     log(f"  errors vs float64 oracle: max_abs={worst['max_abs']:.3e} mean_abs={mean_abs:.3e}; "
-        f"bf16 reference path ({worst['source']}): max_abs={worst['ref_max_abs']:.3e} mean_abs={ref_mean:.3e}")
+        f"bf16 reference path ({worst['source']}): max_abs={worst['ref_max_abs']:.3e} mean_abs={ref_mean:.3e}; "
+        f"ratios max {worst['max_abs'] / worst['ref_max_abs']:.3f} mean {mean_abs / ref_mean:.3f}")
     assert worst["max_abs"] <= MAX_ABS
     assert mean_abs <= MEAN_ABS
-    assert ours_mean_on_ref_rows <= BF16_SLACK * ref_mean
-    assert worst["max_abs"] <= BF16_SLACK * worst["ref_max_abs"] or worst["max_abs"] <= 2 ** -8
+    assert mean_abs <= BF16_SLACK * ref_mean
+    assert worst["max_abs"] <= BF16_SLACK * worst["ref_max_abs"]
 
 
 @torch.inference_mode()

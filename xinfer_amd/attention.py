@@ -4,7 +4,7 @@ Mirror of the reference loader compiler/common/attention.py:1-112: the same
 public names, arguments, errors and fake (meta) functions, so the reference's
 adapters, exporter and tests bind to this module unchanged.  The library is the
 hipcc-built libxinfer_attention_ops.so of this package (xinfer_amd/build.py),
-which registers three operators in the `xinfer` namespace:
+which registers these operators in the `xinfer` namespace:
 
 * ``flash_attention`` and ``batched_flash_attention`` -- read-only attention
   over each request's populated KV prefix (HIP kernels for gfx950);
@@ -54,7 +54,7 @@ _loaded = None
 
 
 def require(condition, message):
-    """Validate external inputs even when Python assertions are disabled."""
+    """Raise ValueError(message) unless condition holds (a check that survives ``python -O``)."""
     if not condition:
         raise ValueError(message)
 
@@ -66,7 +66,12 @@ def default_build_dir(model):
 
 
 def cache_extent(valid_length):
-    """Only this CPU tensor's shape is read; +1 avoids AOTI's size-one guards."""
+    """CPU uint8 tensor of length valid_length + 1 that carries L to flash_attention.
+
+    The operator reads nothing but its length.  The extra element keeps the
+    length at 2 or more, so AOTInductor never specialises it as a size-one
+    dimension.
+    """
     import torch
 
     return torch.empty(valid_length + 1, dtype=torch.uint8)
@@ -87,12 +92,25 @@ def batched_attention_metadata(kv_lengths, query_lengths, device):
         (torch.zeros((2, 1), dtype=torch.int32), lengths.cumsum(1, dtype=torch.int32)), dim=1
     )
     blocks = torch.arange(kv_lengths.shape[0], device=device, dtype=torch.int32)[:, None]
-    if torch.device(device).type == "cuda":
-        # Pinned source: the copy is queued on the current stream without
-        # blocking the host, and is a capturable graph node.
+    if torch.device(device).type == "cuda" and not _tracing():
+        # Eager serving: a pinned source lets the copy queue on the current
+        # stream without blocking the host, and makes it a capturable graph
+        # node.  A traced graph (torch.export, torch.compile) records the plain
+        # copy instead: fake tensors have no pinned storage.
         offsets = offsets.pin_memory()
         return offsets, offsets.to(device, non_blocking=True), blocks
     return offsets, offsets.to(device), blocks
+
+
+def _tracing():
+    """True while torch.export / torch.compile trace the caller, or under a fake mode."""
+    import torch
+
+    if torch.compiler.is_compiling():
+        return True
+    from torch._guards import detect_fake_mode
+
+    return detect_fake_mode() is not None
 
 
 def load_attention_ops(library=None, *, model=None):
@@ -124,7 +142,9 @@ def load_attention_ops(library=None, *, model=None):
 
     @torch.library.register_fake("xinfer::flash_attention")
     def fake(q, k, v, kv_extent, scale):
-        # Valid-prefix length is checked natively; output metadata depends only on Q.
+        # Shapes, dtypes and devices only: the valid length (kv_extent's
+        # length) is validated by the native operator, and the output takes
+        # q's shape and dtype.
         torch._check(q.dim() == 4 and k.dim() == 4 and v.dim() == 4)
         torch._check(q.shape[0] > 0)
         torch._check(q.shape[1] > 0)
@@ -193,7 +213,7 @@ def load_attention_ops(library=None, *, model=None):
 
 
 def attention_library():
-    """Return the implementation selected by the eager/export adapter."""
+    """Path of the library loaded in this process, which export embeds in its packages."""
     require(_loaded is not None, "Load the native attention library before export")
     return _loaded
 

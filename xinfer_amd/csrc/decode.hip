@@ -129,7 +129,11 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
   const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
   const auto rv = buffer_rsrc(a.v.p + it.b * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
   const int first = it.t0 + wave * S::TOK_WAVE + slot;  // this lane's first key row
-  const uint32_t vk = (uint32_t)first * row_bytes_k + dc * 16, vv = (uint32_t)first * row_bytes_v + dc * 16;
+  // Lanes past D (padded head dims) re-read the row's last chunk: bytes of the
+  // row itself, never the gap after it (which a padded view may fill with
+  // anything); their query features are zero and their sums are not written.
+  const uint32_t dcc = dc * 8 < a.D ? (uint32_t)dc : (uint32_t)(a.D / 8 - 1);
+  const uint32_t vk = (uint32_t)first * row_bytes_k + dcc * 16, vv = (uint32_t)first * row_bytes_v + dcc * 16;
 #pragma unroll
   for (int nb = 0; nb < S::NB; ++nb) {
 #pragma unroll

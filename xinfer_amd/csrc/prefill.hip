@@ -39,10 +39,14 @@
 //   A lane l: row l%32, k = 8*(l/32) + 0..7      B lane l: col l%32, same k
 //   C lane l, reg r: row 8*(r/4) + 4*(l/32) + r%4, col l%32
 //
-// Softmax rescaling is lazy: a column's running max m only moves when a tile's
-// max exceeds it by more than kRescaleSlack (log2 units), so most tiles skip
-// the accumulator rescale.  Weights exp2(s - m) then stay below 2^kRescaleSlack;
-// O and the normaliser use the same m, so the quotient is unchanged.
+// Softmax rescaling is exact: whenever a tile raises a column's running max m,
+// m becomes that tile max and the accumulator is rescaled (tiles that raise no
+// column's max skip the rescale).  The key holding a column's maximum score
+// then gets the weight exp2(0) = 1, exact in bf16.  A lazier rule (move m
+// only when the tile max exceeds it by several log2 units) rounds that
+// dominant weight to bf16 as well; on the 512-token chunk at offset 1536 it
+// raised the worst output error from 7.5e-4 to 1.3e-3, above ATen
+// FlashAttention's own bf16 error on the same inputs.
 //
 // Several splits of a tile write fp32 partial records, combined by merge.hip;
 // a tile's records per split are laid out [D/4][128 vectors][4 features].
@@ -54,7 +58,6 @@ namespace xattn {
 
 constexpr int kTileQ = 128;  // query vectors per work item
 constexpr int kBN = 64;      // keys per LDS tile
-constexpr float kRescaleSlack = 8.0f;
 
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) void lds_void;
@@ -366,7 +369,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
     const float mt = pair_max32(mx) * c;  // tile max of the column, log2 units
-    if (__builtin_amdgcn_ballot_w64(mt > m_run + kRescaleSlack)) {
+    if (__builtin_amdgcn_ballot_w64(mt > m_run)) {
       const float m_new = fmaxf(m_run, mt);
       const float alpha = fast_exp2(m_run - (m_new == -INFINITY ? 0.0f : m_new));
       l_run *= alpha;
