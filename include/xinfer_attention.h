@@ -42,7 +42,8 @@ enum {
   XINFER_ERR_LAUNCH = 13,         /* a HIP kernel launch failed */
   XINFER_ERR_ARGUMENT = 14,       /* null pointer or negative size */
   XINFER_ERR_ROPE_SHAPE = 15,     /* xinfer_qk_norm_rope_append shapes (no reference message) */
-  XINFER_ERR_EPS = 16             /* RMSNorm epsilon not finite and >= 0 (no reference message) */
+  XINFER_ERR_EPS = 16,            /* RMSNorm epsilon not finite and >= 0 (no reference message) */
+  XINFER_ERR_SCRATCH = 17         /* the call needs more than XINFER_NOALLOC_SCRATCH_BYTES of scratch */
 };
 
 /* A strided rank-4 view of bf16 device memory, [batch, heads, sequence, dim].
@@ -99,6 +100,23 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
                                        const xinfer_view4 *v, const int32_t *host_offsets,
                                        double scale, const xinfer_view4 *out, void *workspace,
                                        size_t workspace_bytes, void *stream);
+
+/* Allocation-free variant of xinfer_batched_flash_attention.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory or pass
+ * a workspace -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc.  Same arguments, checks, kernels and results as
+ * xinfer_batched_flash_attention, bit for bit; the split records go to a
+ * static device array of the library (one per GPU, held until the process
+ * ends) instead of a caller's workspace, and the call allocates nothing.
+ * A call whose records exceed XINFER_NOALLOC_SCRATCH_BYTES (the size
+ * xinfer_batched_flash_attention_workspace_size reports) returns
+ * XINFER_ERR_SCRATCH and launches nothing.  The current device must be the
+ * stream's.  Calls that overlap in time on one GPU share its array and race:
+ * order them on one stream. */
+#define XINFER_NOALLOC_SCRATCH_BYTES (32u << 20)
+int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_view4 *k,
+                                           const xinfer_view4 *v, const int32_t *host_offsets,
+                                           double scale, void *out, void *stream);
 
 /* ---------------------------------------------------------------------------
  * xinfer::append_kv_batched -- replaces the Triton op

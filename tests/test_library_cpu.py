@@ -52,6 +52,7 @@ def declared_functions():
     for header in HEADERS:
         text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
         text = re.sub(r"//[^\n]*", "", text)
+        text = re.sub(r"^\s*#[^\n]*", "", text, flags=re.M)  # preprocessor lines
         for match in re.finditer(r"\b([A-Za-z_]\w*)\s*\([^;{}]*\)\s*;", text):
             names.append(match.group(1))
     return names
@@ -73,7 +74,7 @@ def test_every_declared_symbol_is_exported(lib):
             "xinfer_qk_norm_rope_append", "xinfer_batched_flash_attention_out", "xinfer_projection_gemv",
             "aoti_torch_cuda_projection_gemv", "aoti_torch_cuda_flash_attention",
             "aoti_torch_cuda_batched_flash_attention", "aoti_torch_cuda_append_kv_batched",
-            "aoti_torch_cuda_qk_norm_rope_append"} <= set(names)
+            "aoti_torch_cuda_qk_norm_rope_append", "xinfer_batched_flash_attention_noalloc"} <= set(names)
     for name in names:
         assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
 
@@ -188,6 +189,35 @@ def test_workspace_size_is_a_pure_host_query(lib):
     # One short row with one split needs no partial records.
     q1, k1 = view([1, 16, 1, 128]), view([1, 8, 4096, 128])
     assert lib.xinfer_flash_attention_workspace_size(ctypes.byref(q1), ctypes.byref(k1), ctypes.c_int64(100)) == 0
+
+
+def test_noalloc_rejects_plans_beyond_its_scratch_before_any_launch(lib):
+    """The allocation-free entry point validates like the workspace one and
+    refuses a plan whose split records exceed its static scratch (32 MiB)
+    with its own status, before any HIP call."""
+    assert lib.xinfer_status_string(17).decode().startswith("Attention needs more split-record scratch")
+    counts = [356, 138, 422, 459, 325, 298, 113, 124]
+    lengths = [14244, 13896, 2059, 4214, 12262, 14086, 12837, 9315]
+    q, k = view([8, 16, 512, 256]), view([8, 4, 16384, 256])
+    offsets = [0]
+    for count in counts:
+        offsets.append(offsets[-1] + count)
+    offsets.append(0)
+    for length in lengths:
+        offsets.append(offsets[-1] + length)
+    host = (ctypes.c_int32 * len(offsets))(*offsets)
+    assert lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(q), ctypes.byref(k), host) > 32 << 20
+
+    def noalloc(qv, kv, offsets_, scale=1.0):
+        return lib.xinfer_batched_flash_attention_noalloc(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),
+                                                          offsets_, ctypes.c_double(scale),
+                                                          ctypes.c_void_p(1 << 20), None)
+
+    assert noalloc(q, k, host) == 17
+    # The checks of the workspace entry point come first, with its codes.
+    assert noalloc(q, k, host, scale=float("nan")) == 7
+    bad = (ctypes.c_int32 * len(offsets))(*([1] + offsets[1:]))
+    assert noalloc(q, k, bad) == 8
 
 
 def prefill_records(lib, counts, lengths, hq, hkv, d, capacity):

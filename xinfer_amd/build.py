@@ -27,7 +27,7 @@ OBJ_DIR = PACKAGE / "_build"
 LIBRARY_NAME = "libxinfer_attention_ops.so"
 ARCH = "gfx950"
 
-KERNEL_SOURCES = ("append.hip", "decode.hip", "prefill.hip", "merge.hip", "norm_rope.hip", "gemv.hip")
+KERNEL_SOURCES = ("append.hip", "decode.hip", "prefill.hip", "merge.hip", "norm_rope.hip", "gemv.hip", "scratch.hip")
 HOST_SOURCES = ("capi.cpp",)
 TORCH_SOURCES = ("torch_ops.cpp",)
 

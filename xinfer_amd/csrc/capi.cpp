@@ -413,6 +413,8 @@ const char *xinfer_status_string(int status) {
     case XINFER_ERR_ROPE_SHAPE:
       return "Expected q [B,Hq,T,D], key/value [B,Hkv,T,D] and cos/sin [B,1,T,D] with D in {64,128,256}";
     case XINFER_ERR_EPS: return "RMSNorm epsilon must be finite and non-negative";
+    case XINFER_ERR_SCRATCH:
+      return "Attention needs more split-record scratch than the allocation-free entry point holds (32 MiB)";
     default: return "Unknown xinfer status";
   }
 }
@@ -439,6 +441,26 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
   return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
+                  static_cast<hipStream_t>(stream));
+}
+
+int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_view4 *k,
+                                           const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                           void *out, void *stream) {
+  static_assert(kScratchBytes == XINFER_NOALLOC_SCRATCH_BYTES, "scratch size of the C header");
+  Geometry g;
+  std::vector<int32_t> counts, lengths;
+  if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
+  if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (g.B == 0 || g.T == 0) return XINFER_OK;
+  if (out == nullptr) return XINFER_ERR_ARGUMENT;
+  const Plan plan = make_plan(g, counts, lengths);
+  if (plan.bytes() > kScratchBytes) return XINFER_ERR_SCRATCH;
+  // The device address of the static scratch on the current device (never
+  // the host-side name of the array).
+  void *records = nullptr;
+  if (plan.bytes() > 0 && scratch_pointer(&records) != hipSuccess) return XINFER_ERR_LAUNCH;
+  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), records,
                   static_cast<hipStream_t>(stream));
 }
 

@@ -22,4 +22,11 @@ hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream);
 // Merges a.total_items query vectors; max_splits picks the thread layout.
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream);
 
+// Bytes of the static device scratch behind the allocation-free entry point
+// (XINFER_NOALLOC_SCRATCH_BYTES of the C header).
+constexpr size_t kScratchBytes = size_t(32) << 20;
+// The current device's address of that scratch (scratch.hip), looked up once
+// per device.
+hipError_t scratch_pointer(void **pointer);
+
 }  // namespace xattn
