@@ -1,6 +1,6 @@
 """Benchmark of the xinfer attention hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--all] [--norm-rope] [--gemv] [--no-cpu-baseline]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--all] [--norm-rope] [--gemv] [--no-cpu-baseline]
 
 A step is one pass of the hot path over one batch: the in-place KV append of
 each row's new tokens followed by one attention call over the populated
@@ -11,7 +11,9 @@ tensors resident in HBM before timing starts.
 The headline workload is BASELINE.json configs[1] (512-token chunked prefill
 at offset 1536, Qwen3-0.6B shapes): ``value`` is its whole-step TFLOP/s.  The
 same line carries the ragged batch-8 decode (configs[2], seed 0) as
-``decode`` with its KV GB/s, and with ``--all`` every configuration.
+``decode`` with its KV GB/s, every other configuration under ``configs``
+(configs[0], [3], [4] and the ragged decode at seeds 1-7), the ragged decode
+seeds 0-7 together as ``decode_seeds_0_7``, and a per-workload ``summary``.
 
 Timing: each workload keeps several copies of its caches and rotates through
 them so consecutive steps never find their KV in the 256 MB Infinity Cache.
@@ -22,9 +24,11 @@ separately with HIP events on the launch stream around graph replays of the
 attention operator alone, and divides the algorithmic work (KV bytes for
 decode, causal FLOPs for prefill) by that average duration.
 
-The CPU baseline times the numpy oracle (fp32) on the host cores over a
-bounded sample of the same workload, and torch's CPU SDPA on bf16 tensors
-(the reference CPU path), both with thread counts.
+The CPU baseline (``cpu_baseline``, headline and decode workloads) times the
+reference CPU path on the host over one full step: an index_copy_ append and
+torch SDPA on bf16 with the explicit lower-right mask, with all threads
+(``value``), with one thread, in fp32, and the numpy oracle, each with its
+thread count.
 """
 
 from __future__ import annotations
@@ -139,6 +143,17 @@ def measured_traffic(w):
     return None if entry is None else entry["bytes"]
 
 
+def cache_copies(w):
+    """Cache copies a workload rotates through so that no step finds its K/V in the MALL.
+
+    Between two uses of one copy the other copies' populated K/V are read:
+    at least twice the 256 MB Infinity Cache, hence ceil(2 * MALL / populated)
+    + 1 copies (2 for the largest workloads).  Each copy is a full-capacity
+    cache, at most 0.54 GB here, so the copies fit comfortably in HBM.
+    """
+    return max(2, -(-2 * MALL_BYTES // max(w.kv_bytes(), 1)) + 1)
+
+
 class Runner:
     """Device state of one workload: rotating cache copies and captured step graphs."""
 
@@ -149,15 +164,13 @@ class Runner:
 
         self.w, self.torch = w, torch
         device = "cuda"
-        populated = w.kv_bytes()
-        self.copies = max(2, min(8, -(-2 * MALL_BYTES // max(populated, 1)) + 1))
+        self.copies = cache_copies(w)
         self.q = inputs["q"].to(device)
         self.new_k = inputs["new_k"].to(device)
         self.new_v = inputs["new_v"].to(device)
         self.positions = inputs["positions"].to(device)
-        self.caches = []
-        for _ in range(self.copies):
-            self.caches.append((inputs["k"].to(device), inputs["v"].to(device)))
+        k, v = inputs["k"].to(device), inputs["v"].to(device)
+        self.caches = [(k, v)] + [(k.clone(), v.clone()) for _ in range(self.copies - 1)]
         counts = torch.tensor(w.counts, dtype=torch.int32)
         lengths = torch.tensor(w.lengths, dtype=torch.int32)
         self.host, self.cu, self.blocks = batched_attention_metadata(lengths, counts, device)
@@ -269,7 +282,20 @@ class Runner:
 
 
 def cpu_baseline(w, inputs, budget_s):
-    """Oracle (fp32 numpy) and torch CPU SDPA (bf16) on a bounded sample of the workload."""
+    """The reference CPU path and the oracle, timed on the host over one full step of the workload.
+
+    Legs (median of repeated runs, each leg bounded by ``budget_s`` seconds):
+
+    * ``sdpa_bf16``: the reference's CPU path: per row
+      an index_copy_ of the new K/V into a CPU cache of the same capacity, then
+      torch SDPA on bf16 tensors with the explicit lower-right mask and
+      enable_gqa, with all of torch's threads;
+    * ``sdpa_bf16_1thread``: the same with one thread (the reference runtime
+      runs on one CPU thread);
+    * ``sdpa_fp32``: the same in fp32 (the precision of the reference tests'
+      own oracle);
+    * ``oracle_fp32``: this repository's numpy oracle in fp32 (attention only).
+    """
     import numpy as np
     import torch
     import torch.nn.functional as F
@@ -277,28 +303,39 @@ def cpu_baseline(w, inputs, budget_s):
 
     from oracle import attention as oracle
 
-    rows = list(range(w.batch))
+    rows = [r for r in range(w.batch) if w.counts[r] > 0]
     counts = [w.counts[r] for r in rows]
     lengths = [w.lengths[r] for r in rows]
-    # The sample: the rows' populated prefixes, widened once (resident inputs).
-    q = [inputs["q"][r : r + 1, :, : counts[i]].float().numpy() for i, r in enumerate(rows)]
-    k = [inputs["k_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
-    v = [inputs["v_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
+
+    def row_caches(dtype):
+        return [(inputs["k"][r : r + 1].to(dtype).clone(), inputs["v"][r : r + 1].to(dtype).clone()) for r in rows]
+
+    def sdpa_step(dtype):
+        caches = row_caches(dtype)
+        q = [inputs["q"][r : r + 1, :, : counts[i]].to(dtype) for i, r in enumerate(rows)]
+        new = [(inputs["new_k"][r : r + 1, :, : counts[i]].to(dtype), inputs["new_v"][r : r + 1, :, : counts[i]].to(dtype))
+               for i, r in enumerate(rows)]
+        positions = [inputs["positions"][r, : counts[i]] for i, r in enumerate(rows)]
+        masks = [torch.arange(L)[None, :] <= torch.arange(L - n, L)[:, None] for n, L in zip(counts, lengths)]
+
+        def step():
+            with sdpa_kernel(SDPBackend.MATH):
+                for i in range(len(rows)):
+                    k, v = caches[i]
+                    if w.append:
+                        k.index_copy_(2, positions[i], new[i][0])
+                        v.index_copy_(2, positions[i], new[i][1])
+                    F.scaled_dot_product_attention(q[i], k[:, :, : lengths[i]], v[:, :, : lengths[i]],
+                                                   attn_mask=masks[i], enable_gqa=True, scale=w.scale)
+        return step
+
+    qf = [inputs["q"][r : r + 1, :, : counts[i]].float().numpy() for i, r in enumerate(rows)]
+    kf = [inputs["k_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
+    vf = [inputs["v_after"][r : r + 1, :, : lengths[i]].float().numpy() for i, r in enumerate(rows)]
 
     def oracle_step():
         for i in range(len(rows)):
-            oracle.attention(q[i], k[i], v[i], [counts[i]], [lengths[i]], w.scale, dtype=np.float32)
-
-    qb = [inputs["q"][r : r + 1, :, : counts[i]] for i, r in enumerate(rows)]
-    kb = [inputs["k_after"][r : r + 1, :, : lengths[i]] for i, r in enumerate(rows)]
-    vb = [inputs["v_after"][r : r + 1, :, : lengths[i]] for i, r in enumerate(rows)]
-    masks = [torch.arange(L)[None, :] <= torch.arange(L - n, L)[:, None] for n, L in zip(counts, lengths)]
-
-    def sdpa_step():
-        with sdpa_kernel(SDPBackend.MATH):
-            for i in range(len(rows)):
-                F.scaled_dot_product_attention(qb[i], kb[i], vb[i], attn_mask=masks[i], enable_gqa=True,
-                                               scale=w.scale)
+            oracle.attention(qf[i], kf[i], vf[i], [counts[i]], [lengths[i]], w.scale, dtype=np.float32)
 
     def timeit(function):
         function()  # warm-up
@@ -309,16 +346,26 @@ def cpu_baseline(w, inputs, budget_s):
             function()
             times.append(time.perf_counter() - start)
         times.sort()
-        return times[len(times) // 2], len(times)
+        return dict(seconds=times[len(times) // 2], runs=len(times))
 
-    oracle_s, oracle_reps = timeit(oracle_step)
-    sdpa_s, sdpa_reps = timeit(sdpa_step)
+    threads = torch.get_num_threads()
+    legs = {"sdpa_bf16": timeit(sdpa_step(torch.bfloat16))}
+    legs["sdpa_bf16"]["threads"] = threads
+    legs["sdpa_fp32"] = timeit(sdpa_step(torch.float32))
+    legs["sdpa_fp32"]["threads"] = threads
+    torch.set_num_threads(1)
+    try:
+        legs["sdpa_bf16_1thread"] = timeit(sdpa_step(torch.bfloat16))
+        legs["sdpa_bf16_1thread"]["threads"] = 1
+    finally:
+        torch.set_num_threads(threads)
+    legs["oracle_fp32"] = timeit(oracle_step)
     try:
         from threadpoolctl import threadpool_info
 
-        blas_threads = max((info.get("num_threads", 1) for info in threadpool_info()), default=1)
+        legs["oracle_fp32"]["threads"] = max((info.get("num_threads", 1) for info in threadpool_info()), default=1)
     except Exception:
-        blas_threads = os.cpu_count()
+        legs["oracle_fp32"]["threads"] = os.cpu_count()
     cpu_model = ""
     try:
         for line in Path("/proc/cpuinfo").read_text().splitlines():
@@ -327,9 +374,7 @@ def cpu_baseline(w, inputs, budget_s):
                 break
     except OSError:
         pass
-    return dict(oracle_s=oracle_s, oracle_reps=oracle_reps, sdpa_s=sdpa_s, sdpa_reps=sdpa_reps,
-                blas_threads=blas_threads, torch_threads=torch.get_num_threads(), cpu_model=cpu_model,
-                os_cpus=os.cpu_count())
+    return dict(legs=legs, cpu_model=cpu_model, os_cpus=os.cpu_count())
 
 
 def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
@@ -379,27 +424,23 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
         f"attention op {op_seconds * 1e6:.1f} us = {achieved:.1f} {unit} ({100 * achieved / peak:.1f}% of peak)")
     if with_cpu:
         cpu = cpu_baseline(w, inputs, cpu_budget)
+        legs = cpu["legs"]
+        main = legs["sdpa_bf16"]
         result["cpu_baseline"] = {
-            "value": work / cpu["oracle_s"] / scale,
+            "value": work / main["seconds"] / scale,
             "unit": unit,
-            "cores": cpu["blas_threads"],
-            "kind": "port",
-            "sample": f"one full step of {w.name} (all {w.batch} rows, fp32 numpy oracle), "
-                      f"median of {cpu['oracle_reps']} runs",
-            "reference_cpu_sdpa": {
-                "value": work / cpu["sdpa_s"] / scale,
-                "unit": unit,
-                "threads": cpu["torch_threads"],
-                "dtype": "bf16",
-                "median_ms": cpu["sdpa_s"] * 1e3,
-                "runs": cpu["sdpa_reps"],
-            },
+            "cores": main["threads"],
+            "kind": "reference",
+            "sample": f"one full step of {w.name} on the host: per row index_copy_ append into a CPU cache of the "
+                      f"same capacity, then torch CPU SDPA on bf16 with the explicit lower-right mask "
+                      f"(the reference's CPU attention path); median of {main['runs']} runs",
+            "legs": {name: {"value": work / leg["seconds"] / scale, "unit": unit, "median_ms": leg["seconds"] * 1e3,
+                            "runs": leg["runs"], "threads": leg["threads"]} for name, leg in legs.items()},
             "cpu_model": cpu["cpu_model"],
             "os_cpu_count": cpu["os_cpus"],
         }
-        log(f"[bench] {w.name}: CPU oracle {result['cpu_baseline']['value']:.3g} {unit} "
-            f"({cpu['blas_threads']} threads); CPU SDPA bf16 {work / cpu['sdpa_s'] / scale:.3g} {unit} "
-            f"({cpu['torch_threads']} threads)")
+        log(f"[bench] {w.name}: CPU " + ", ".join(
+            f"{name} {work / leg['seconds'] / scale:.3g} {unit} ({leg['threads']} threads)" for name, leg in legs.items()))
     del runner
     torch.cuda.empty_cache()
     return result
@@ -554,7 +595,9 @@ def main():
     parser.add_argument("--steps", type=int, default=200)
     parser.add_argument("--warmup", type=int, default=20)
     parser.add_argument("--all", action="store_true",
-                        help="also measure configs 1, 4, 5, cfg3 seeds 0-7 and the fused norm/rope/append step")
+                        help="also time the fused norm/rope/append step and the projection GEMV")
+    parser.add_argument("--quick", action="store_true",
+                        help="only the headline prefill and the cfg3 seed-0 decode (no other configs)")
     parser.add_argument("--norm-rope", action="store_true",
                         help="only time the fused norm/rope/append step against the eager modules and print "
                              "its JSON (cfg2 and cfg3 token shapes)")
@@ -600,7 +643,7 @@ def main():
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     extra = []
-    if args.all:
+    if not args.quick:
         for index, seed in [(1, 0), (4, 0), (5, 0)] + [(3, s) for s in range(1, 8)]:
             extra.append(measure(index, seed, args.steps, args.warmup, not args.eager, False, args.cpu_budget))
     line = {
@@ -638,6 +681,10 @@ def main():
                                     "GBs": round(moved / op_us / 1e3, 1),
                                     "frac_hbm": round(moved / op_us / 1e3 / HBM_PEAK_GBS, 4)}
         log(f"[bench] cfg3 seeds 0-7 aggregate: {moved} B in {op_us:.1f} us = {moved / op_us / 1e3:.1f} GB/s")
+        line["summary"] = {r["workload"]: {"attention_op_us": round(r["attention_op_us"], 2),
+                                           "achieved": round(r["roofline"]["achieved"], 1),
+                                           "unit": r["unit"], "frac": round(r["roofline"]["frac"], 4)}
+                           for r in [prefill, decode] + extra}
     if args.all:
         line["norm_rope"] = [measure_norm_rope(2, 0), measure_norm_rope(3, 0)]
         line["projection_gemv"] = measure_gemv()
