@@ -157,7 +157,7 @@ def cache_copies(w):
 class Runner:
     """Device state of one workload: rotating cache copies and captured step graphs."""
 
-    def __init__(self, w, inputs, use_graphs=True):
+    def __init__(self, w, inputs, use_graphs=True, graph_op=False):
         import torch
 
         from xinfer_amd.attention import batched_attention_metadata, cache_extent
@@ -179,10 +179,13 @@ class Runner:
         self.use_graphs = use_graphs
         self.step_graphs = self.cycle_graph = self.attention_graph = None
         self.cycle = self.copies
+        self.graph_op = graph_op
 
     def attention(self, i):
         ops = self.torch.ops.xinfer
         k, v = self.caches[i % self.copies]
+        if self.graph_op:
+            return ops.batched_flash_attention_graph(self.q, k, v, self.host, self.cu, self.blocks, self.w.scale)
         if self.w.op == "flash":
             return ops.flash_attention(self.q, k, v, self.extent, self.w.scale)
         return ops.batched_flash_attention(self.q, k, v, self.host, self.cu, self.blocks, self.w.scale)
@@ -566,6 +569,38 @@ def measure_gemv(replays=20, per_graph=50):
     return results
 
 
+def measure_graph_decode(steps, warmup):
+    """The graph-capture operator (lengths read on the device, launch sized
+    for the capacity) against the default operator (launch planned from host
+    lengths) on the decode workloads: attention-op time of each, from HIP
+    events around graph replays as in the main line."""
+    import torch
+
+    from xinfer_amd import workloads
+
+    results = []
+    for index, seed in [(3, s) for s in range(8)] + [(4, 0)]:
+        w = workloads.config(index, seed)
+        inputs = workloads.make_inputs(w)
+        times = {}
+        for mode in ("default", "graph"):
+            runner = Runner(w, inputs, True, graph_op=mode == "graph")
+            with torch.inference_mode():
+                runner.capture()
+                runner.run_steps(warmup)
+                times[mode] = runner.attention_duration(max(steps, 4 * runner.copies))
+            del runner
+            torch.cuda.empty_cache()
+        results.append({"workload": w.name, "default_us": round(times["default"] * 1e6, 2),
+                        "graph_us": round(times["graph"] * 1e6, 2),
+                        "graph_GBs": round(w.kv_bytes() / times["graph"] / 1e9, 1)})
+        log(f"[bench] graph-capture decode {w.name}: default {times['default'] * 1e6:.1f} us, "
+            f"graph mode {times['graph'] * 1e6:.1f} us")
+    default = sum(r["default_us"] for r in results if r["workload"].startswith("cfg3_"))
+    graph = sum(r["graph_us"] for r in results if r["workload"].startswith("cfg3_"))
+    return {"graph_decode": results, "cfg3_seeds_0_7_us": {"default": round(default, 2), "graph": round(graph, 2)}}
+
+
 COPY_PROBE_BYTES = 256 << 20
 
 
@@ -603,6 +638,8 @@ def main():
                              "its JSON (cfg2 and cfg3 token shapes)")
     parser.add_argument("--gemv", action="store_true",
                         help="only time xinfer::projection_gemv against F.linear on the decoder geometries")
+    parser.add_argument("--graph-decode", action="store_true",
+                        help="only time the graph-capture operator against the default one on the decode workloads")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
@@ -638,6 +675,9 @@ def main():
         return
     if args.gemv:
         print(json.dumps({"projection_gemv": measure_gemv()}), flush=True)
+        return
+    if args.graph_decode:
+        print(json.dumps(measure_graph_decode(args.steps, args.warmup)), flush=True)
         return
     with_cpu = not args.no_cpu_baseline
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)

@@ -74,7 +74,8 @@ def test_every_declared_symbol_is_exported(lib):
             "xinfer_qk_norm_rope_append", "xinfer_batched_flash_attention_out", "xinfer_projection_gemv",
             "aoti_torch_cuda_projection_gemv", "aoti_torch_cuda_flash_attention",
             "aoti_torch_cuda_batched_flash_attention", "aoti_torch_cuda_append_kv_batched",
-            "aoti_torch_cuda_qk_norm_rope_append", "xinfer_batched_flash_attention_noalloc"} <= set(names)
+            "aoti_torch_cuda_qk_norm_rope_append", "xinfer_batched_flash_attention_noalloc",
+            "xinfer_batched_flash_attention_graph"} <= set(names)
     for name in names:
         assert hasattr(lib, name), f"{name} is declared in include/ but not exported"
 
@@ -218,6 +219,31 @@ def test_noalloc_rejects_plans_beyond_its_scratch_before_any_launch(lib):
     assert noalloc(q, k, host, scale=float("nan")) == 7
     bad = (ctypes.c_int32 * len(offsets))(*([1] + offsets[1:]))
     assert noalloc(q, k, bad) == 8
+
+
+def test_graph_mode_shapes_and_workspace(lib):
+    """The graph-capture entry point plans from shapes alone: its workspace
+    holds every row's records at capacity, and rows that would take the
+    prefill kernel (T * Hq/Hkv > 8) or more than 64 rows are refused before
+    any launch."""
+    lib.xinfer_batched_flash_attention_graph_workspace_size.restype = ctypes.c_size_t
+    q, k = view([8, 16, 1, 128]), view([8, 8, 16384, 128])
+    size = lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(q), ctypes.byref(k))
+    splits = 16384 // 128  # keys per decode item at D = 128 with two query vectors per KV head
+    records = 8 * 8 * splits * 2
+    assert size == -(-records * 128 * 4 // 256) * 256 + records * 8
+    assert lib.xinfer_status_string(18).decode().startswith("Graph-capture attention takes decode rows")
+
+    def graph(qv, kv):
+        return lib.xinfer_batched_flash_attention_graph(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),
+                                                        ctypes.c_void_p(1 << 21), ctypes.c_double(0.1),
+                                                        ctypes.c_void_p(1 << 20), None, ctypes.c_size_t(0), None)
+
+    assert graph(view([1, 16, 5, 128]), view([1, 8, 256, 128])) == 18   # 10 query vectors per KV head
+    assert graph(view([65, 16, 1, 128]), view([65, 8, 256, 128])) == 18
+    assert graph(view([1, 16, 1, 128]), view([1, 8, 256, 128])) == 10   # no workspace given
+    assert lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(view([1, 16, 1, 128])),
+                                                                   ctypes.byref(view([1, 8, 128, 128]))) == 0
 
 
 def prefill_records(lib, counts, lengths, hq, hkv, d, capacity):

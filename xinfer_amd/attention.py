@@ -12,6 +12,9 @@ which registers these operators in the `xinfer` namespace:
   reference's Triton op (compiler/common/kernels/kv_cache.py:45-72);
 * ``batched_flash_attention_bthd`` -- ``batched_flash_attention`` with its
   output in [B,T,Hq,D] order (the adapter's reshape then needs no copy);
+* ``batched_flash_attention_graph`` -- ``batched_flash_attention`` for decode
+  batches that are captured once in a HIP graph and replayed while the
+  lengths change: the kernels read the lengths from ``cuda_offsets``;
 * ``projection_gemv`` -- the decoder's singleton projections, native instead
   of the reference's Triton op (compiler/common/kernels/projection_gemv.py);
 * ``qk_norm_rope_append`` -- the step before the attention operator in one
@@ -180,6 +183,13 @@ def load_attention_ops(library=None, *, model=None):
         def fake_batched_bthd(q, k, v, offsets, cuda_offsets, blocks, scale):
             out = fake_batched(q, k, v, offsets, cuda_offsets, blocks, scale)
             return out.new_empty((q.shape[0], q.shape[2], q.shape[1], q.shape[3]))
+
+    if hasattr(torch.ops.xinfer, "batched_flash_attention_graph"):
+
+        @torch.library.register_fake("xinfer::batched_flash_attention_graph")
+        def fake_batched_graph(q, k, v, offsets, cuda_offsets, blocks, scale):
+            torch._check(q.shape[2] * (q.shape[1] // k.shape[1]) <= 8)
+            return fake_batched(q, k, v, offsets, cuda_offsets, blocks, scale)
 
     if hasattr(torch.ops.xinfer, "append_kv_batched"):
 

@@ -374,6 +374,44 @@ int check_batched(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
   return XINFER_OK;
 }
 
+// Graph-capture mode (xinfer_batched_flash_attention_graph): a plan that
+// depends only on the shapes.  Rows must take the decode kernel (at most
+// kDecodeMaxQueryVectors query vectors per KV head, i.e. T * G <= 8) and fit
+// one row table (B <= kMaxRows, which the kernels' per-block tables assume).
+// Records are laid out for every row at capacity.
+struct CapturePlan {
+  int dp = 0, qr = 1, tok_item = 0, splits_max = 0, decode_blocks = 0;
+  int64_t row_records = 0, records = 0;
+  size_t part_ml_offset() const { return (size_t)((records * dp_d * 4 + 255) / 256 * 256); }
+  size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
+  int64_t dp_d = 0;  // the head dim D (records hold D floats)
+};
+// Decode blocks of a capture launch: every item of the capacity layout, at
+// most eight per CU of the 256 (the blocks take the valid items in turn).
+constexpr int kCaptureMaxBlocks = 2048;
+
+int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v, Geometry &g,
+                  CapturePlan &cp) {
+  if (!q || !k || !v) return XINFER_ERR_ARGUMENT;
+  g = Geometry{q->size[0], q->size[1], k->size[1], q->size[2], q->size[3], k->size[2]};
+  bool same = true;
+  for (int i = 0; i < 4; ++i) same = same && v->size[i] == k->size[i];
+  if (!(same && k->size[0] == g.B && k->size[3] == g.D) || g.B < 0 || g.T < 0 || g.C <= 0)
+    return XINFER_ERR_QKV_SHAPES;
+  if (int rc = check_heads_and_dim(g)) return rc;
+  const int64_t G = g.Hq / g.Hkv;
+  if (g.T * G > kDecodeMaxQueryVectors || g.B > kMaxRows) return XINFER_ERR_CAPTURE_ROWS;
+  cp.dp = padded_dim(g.D);
+  cp.dp_d = g.D;
+  cp.qr = pow2_at_least((int)std::max<int64_t>(1, g.T * G));
+  cp.tok_item = decode_tokens_per_item(cp.dp, cp.qr);
+  cp.splits_max = (int)ceil_div(g.C, cp.tok_item);
+  cp.row_records = g.Hkv * cp.splits_max * g.T * G;
+  cp.records = cp.splits_max > 1 ? g.B * cp.row_records : 0;
+  cp.decode_blocks = (int)std::min<int64_t>(std::max<int64_t>(1, g.B * g.Hkv * cp.splits_max), kCaptureMaxBlocks);
+  return XINFER_OK;
+}
+
 int check_common(const xinfer_view4 &q, const xinfer_view4 &k, const xinfer_view4 &v, double scale) {
   if (!(std::isfinite(scale) && scale > 0)) return XINFER_ERR_SCALE;
   if (!attention_layout_ok(q) || !query_layout_ok(q) || !attention_layout_ok(k) ||
@@ -413,6 +451,9 @@ const char *xinfer_status_string(int status) {
     case XINFER_ERR_ROPE_SHAPE:
       return "Expected q [B,Hq,T,D], key/value [B,Hkv,T,D] and cos/sin [B,1,T,D] with D in {64,128,256}";
     case XINFER_ERR_EPS: return "RMSNorm epsilon must be finite and non-negative";
+    case XINFER_ERR_CAPTURE_ROWS:
+      return "Graph-capture attention takes decode rows: at most 8 query vectors per KV head (T * Hq/Hkv) "
+             "and 64 rows";
     case XINFER_ERR_SCRATCH:
       return "Attention needs more split-record scratch than the allocation-free entry point holds (32 MiB)";
     default: return "Unknown xinfer status";
@@ -442,6 +483,53 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
     return XINFER_ERR_WORKSPACE;
   return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
                   static_cast<hipStream_t>(stream));
+}
+
+size_t xinfer_batched_flash_attention_graph_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k) {
+  Geometry g;
+  CapturePlan cp;
+  if (check_capture(q, k, k, g, cp) != XINFER_OK) return 0;
+  return cp.bytes();
+}
+
+int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
+                                         const int32_t *device_offsets, double scale, void *out, void *workspace,
+                                         size_t workspace_bytes, void *stream) {
+  Geometry g;
+  CapturePlan cp;
+  if (int rc = check_capture(q, k, v, g, cp)) return rc;
+  if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (g.B == 0 || g.T == 0) return XINFER_OK;
+  if (out == nullptr || device_offsets == nullptr) return XINFER_ERR_ARGUMENT;
+  if (workspace_bytes < cp.bytes() || (cp.bytes() && workspace == nullptr)) return XINFER_ERR_WORKSPACE;
+  CaptureArgs c{};
+  c.q = view_of(*q);
+  c.k = view_of(*k);
+  c.v = view_of(*v);
+  c.out = static_cast<uint16_t *>(out);
+  c.o_sb = g.Hq * g.T * g.D;
+  c.o_sh = g.T * g.D;
+  c.o_st = g.D;
+  c.part_o = static_cast<float *>(workspace);
+  c.part_ml = cp.records ? reinterpret_cast<float *>(static_cast<char *>(workspace) + cp.part_ml_offset()) : nullptr;
+  c.offsets = device_offsets;
+  c.scale_log2 = (float)(scale * 1.4426950408889634);
+  c.D = (int32_t)g.D;
+  c.G = (int32_t)(g.Hq / g.Hkv);
+  c.Hkv = (int32_t)g.Hkv;
+  c.T = (int32_t)g.T;
+  c.B = (int32_t)g.B;
+  c.C = (int32_t)g.C;
+  c.tok_item = cp.tok_item;
+  c.row_records = cp.row_records;
+  c.total_items = (int32_t)(g.B * g.Hkv * cp.splits_max);
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (launch_decode_capture(c, cp.dp, cp.qr, cp.decode_blocks, s) != hipSuccess) return XINFER_ERR_LAUNCH;
+  if (cp.splits_max > 1) {
+    c.total_items = (int32_t)(g.B * g.Hkv * g.T * c.G);
+    if (launch_merge_capture(c, cp.dp, cp.splits_max, s) != hipSuccess) return XINFER_ERR_LAUNCH;
+  }
+  return XINFER_OK;
 }
 
 int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_view4 *k,

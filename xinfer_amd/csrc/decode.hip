@@ -298,6 +298,76 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   process_item(p, it, r, sh, wave, lane, slot, dc);
 }
 
+// Graph-capture decode: the launch shape depends only on the tensor shapes.
+// Each block reads every row's count and length once, numbers the row's work
+// items as the default schedule would (Hkv x splits, or Hkv zero-fill items
+// for a row without queries), and takes items blockIdx.x, blockIdx.x +
+// gridDim.x, ... of that list, so the valid items are spread evenly over the
+// grid whatever the lengths; blocks past the list exit after the one read.
+template <int DP, int QR>
+__global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c) {
+  using S = DecodeShape<DP, QR>;
+  __shared__ DecodeShared<DP, QR> sh;
+  __shared__ int row_count[kMaxRows], row_length[kMaxRows], row_splits[kMaxRows], row_first[kMaxRows + 1];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int slot = lane / S::LPT, dc = lane % S::LPT;
+  if (tid < c.B) {
+    int count, length;
+    capture_row(c, tid, count, length);
+    row_count[tid] = count;
+    row_length[tid] = length;
+    row_splits[tid] = count == 0 ? 1 : (length + c.tok_item - 1) / c.tok_item;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int first = 0;
+    for (int r = 0; r < c.B; ++r) {
+      row_first[r] = first;
+      first += c.Hkv * row_splits[r];
+    }
+    row_first[c.B] = first;
+  }
+  __syncthreads();
+  const int total = row_first[c.B];
+  const DecodeParams p{c.q, c.k, c.v, c.out, c.o_sb, c.o_sh, c.o_st, c.part_o, c.part_ml, c.scale_log2, c.D, c.G, c.T};
+  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+    int r = 0;
+    while (row_first[r + 1] <= item) ++r;
+    RowSched rs;
+    rs.batch = r;
+    rs.count = row_count[r];
+    rs.length = row_length[r];
+    rs.item_begin = row_first[r];
+    rs.nsplit = row_splits[r];
+    rs.ntiles = 1;
+    rs.rec_begin = (int64_t)r * c.row_records;
+    const DecodeItem it = locate_item(rs, item, S::TOK_ITEM);
+    DecodeRegs<DP, QR> regs;
+    issue_item(p, it, regs, wave, slot, dc);
+    process_item(p, it, regs, sh, wave, lane, slot, dc);
+    __syncthreads();  // the next item reuses the block's reduction buffers
+  }
+}
+
+template <int DP>
+static hipError_t launch_decode_capture_d(const CaptureArgs &c, int qr, int blocks, hipStream_t stream) {
+  switch (qr) {
+    case 1: hipLaunchKernelGGL((decode_capture_kernel<DP, 1>), dim3(blocks), dim3(256), 0, stream, c); break;
+    case 2: hipLaunchKernelGGL((decode_capture_kernel<DP, 2>), dim3(blocks), dim3(256), 0, stream, c); break;
+    case 4: hipLaunchKernelGGL((decode_capture_kernel<DP, 4>), dim3(blocks), dim3(256), 0, stream, c); break;
+    default: hipLaunchKernelGGL((decode_capture_kernel<DP, 8>), dim3(blocks), dim3(256), 0, stream, c); break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int blocks, hipStream_t stream) {
+  switch (dp) {
+    case 64: return launch_decode_capture_d<64>(c, qr, blocks, stream);
+    case 128: return launch_decode_capture_d<128>(c, qr, blocks, stream);
+    default: return launch_decode_capture_d<256>(c, qr, blocks, stream);
+  }
+}
+
 int decode_tokens_per_item(int dp, int qr) {
   const int u = qr <= 2 ? 4 : (qr == 4 ? 2 : 1);
   return 4 * (qr == 8 ? 4 : 8 / u) * (64 / (dp / 8)) * u;

@@ -67,6 +67,26 @@ struct MergeArgs {
   MergeRow rows[kMaxRows];
 };
 
+// Graph-capture decode (decode.hip, merge.hip): one launch shape serves every
+// step, because the kernels read each row's query count and KV length from
+// the device copy of the cumulative offsets instead of a host schedule.
+// Records are laid out per row at capacity: row r's start at r * row_records,
+// in the decode layout [kv head][split][vector] with the row's actual split
+// count.  Counts are clamped to [0, T] and lengths to [max(count, 1), C], so
+// no device data can address outside q, k, v, out or the workspace.
+struct CaptureArgs {
+  View q, k, v;
+  uint16_t *out;             // contiguous [B, Hq, T, D]
+  int64_t o_sb, o_sh, o_st;
+  float *part_o, *part_ml;   // records of every row at capacity
+  const int32_t *offsets;    // device [2][B + 1]: cumulative counts, cumulative lengths
+  float scale_log2;
+  int32_t D, G, Hkv, T, B, C;
+  int32_t tok_item;          // keys per decode work item
+  int32_t total_items;       // decode: items at capacity; merge: query vectors at capacity
+  int64_t row_records;       // records per row at capacity: Hkv * ceil(C / tok_item) * T * G
+};
+
 struct AppendArgs {
   View key, value;
   int64_t key_sd, value_sd;  // feature strides (1 on the vector path)

@@ -48,11 +48,64 @@ __device__ __forceinline__ void fold(MergeState &st, float ms, float ls, f32x4 o
   st.m = mn;
 }
 
+template <int DP, int SG>
+using MergeRed = MergeState[SG > 1 ? SG : 1][SG > 1 ? DP / 4 : 1];
+
+// Folds the nsplit records of one query vector over this thread's 4 features
+// and writes them as bf16 at dst.  Record s: o at part_o + o_base + s * o_step,
+// (m, l) at part_ml + 2 * (ml_base + s * ml_step).  With SG > 1 split lanes
+// per feature group every thread of the block must call it (it synchronises
+// the block); `active` is false for threads past the vectors or features.
+// Every record of a batch is loaded before any is folded: a lane's splits take
+// ceil(nsplit / (SG * INFLIGHT)) memory round trips.
+template <int DP, int SG>
+__device__ __forceinline__ void fold_and_write(MergeRed<DP, SG> &red, const float *part_o, const float *part_ml,
+                                               int64_t o_base, int64_t o_step, int64_t ml_base, int64_t ml_step,
+                                               int nsplit, bool active, int sg, int f, uint16_t *dst) {
+  constexpr int INFLIGHT = SG > 1 ? 16 : 4;
+  MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
+  if (active) {
+    for (int s0 = sg; s0 < nsplit; s0 += INFLIGHT * SG) {
+      u32x2 ml[INFLIGHT];
+      f32x4 o[INFLIGHT];
+#pragma unroll
+      for (int u = 0; u < INFLIGHT; ++u) {
+        const int64_t sp = min(s0 + u * SG, nsplit - 1);
+        ml[u] = *as_global(reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step)));
+        o[u] = *as_global(reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step));
+      }
+#pragma unroll
+      for (int u = 0; u < INFLIGHT; ++u)
+        if (s0 + u * SG < nsplit) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
+    }
+  }
+  if constexpr (SG > 1) {
+    red[sg][f] = st;
+    __syncthreads();
+    if (sg != 0) return;
+    // The states are read eight at a time before they are folded (in split
+    // lane order), so the fold waits for one LDS round trip per eight lanes.
+    for (int k0 = 1; k0 < SG; k0 += 8) {
+      MergeState other[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < SG) other[u] = red[k0 + u][f];
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+        if (k0 + u < SG) fold(st, other[u].m, other[u].l, other[u].o);
+    }
+  }
+  if (!active) return;
+  const float inv = 1.0f / st.l;
+  *as_global(reinterpret_cast<u32x2 *>(dst)) =
+      u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
+}
+
 template <int DP, int SG, int THREADS>
 __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   constexpr int FC = DP / 4;                // feature lanes
   constexpr int VPB = THREADS / (FC * SG);  // query vectors per block
-  __shared__ MergeState red[SG > 1 ? SG : 1][SG > 1 ? FC : 1];
+  __shared__ MergeRed<DP, SG> red;
 
   // Few splits: vectors vary fastest across a block's threads (the prefill
   // record layout keeps a tile's vectors contiguous per feature group).
@@ -99,47 +152,9 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
     o_step = ml_step * D;
   }
 
-  // Every record of a batch is loaded before any is folded: a lane's splits
-  // take ceil(nsplit / (SG * INFLIGHT)) memory round trips.
-  constexpr int INFLIGHT = SG > 1 ? 16 : 4;
-  MergeState st{-INFINITY, 0.0f, f32x4{0.0f, 0.0f, 0.0f, 0.0f}};
-  if (vvalid && d < D) {
-    for (int s0 = sg; s0 < mr.nsplit; s0 += INFLIGHT * SG) {
-      u32x2 ml[INFLIGHT];
-      f32x4 o[INFLIGHT];
-#pragma unroll
-      for (int u = 0; u < INFLIGHT; ++u) {
-        const int64_t sp = min(s0 + u * SG, mr.nsplit - 1);
-        ml[u] = *as_global(reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step)));
-        o[u] = *as_global(reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step));
-      }
-#pragma unroll
-      for (int u = 0; u < INFLIGHT; ++u)
-        if (s0 + u * SG < mr.nsplit) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
-    }
-  }
-  if constexpr (SG > 1) {
-    red[sg][f] = st;
-    __syncthreads();
-    if (sg != 0) return;
-    // The states are read eight at a time before they are folded (in split
-    // lane order), so the fold waits for one LDS round trip per eight lanes.
-    for (int k0 = 1; k0 < SG; k0 += 8) {
-      MergeState other[8];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k0 + u < SG) other[u] = red[k0 + u][f];
-#pragma unroll
-      for (int u = 0; u < 8; ++u)
-        if (k0 + u < SG) fold(st, other[u].m, other[u].l, other[u].o);
-    }
-  }
-  if (!vvalid || d >= D) return;
-  const float inv = 1.0f / st.l;
   const int g = j % G, i = j / G;
-  uint16_t *dst = out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st;
-  *as_global(reinterpret_cast<u32x2 *>(dst + d)) =
-      u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
+  fold_and_write<DP, SG>(red, part_o, part_ml, o_base, o_step, ml_base, ml_step, mr.nsplit, vvalid && d < D, sg, f,
+                         out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st + d);
 }
 
 // Splits at or below this count use one thread per (vector, 4 features).
@@ -165,6 +180,55 @@ static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t
       hipLaunchKernelGGL((merge_kernel<DP, 1024 / FC, 1024>), grid, dim3(1024), 0, stream, a);
   }
   return hipGetLastError();
+}
+
+// Graph-capture merge: one block per query vector of the capacity layout
+// (row, kv head, vector j < T * G), with split lanes over the splits.  The
+// row's count and length come from the device offsets; vectors past the row's
+// queries and rows whose keys fit one item (written by the decode kernel
+// directly) have nothing to merge.
+template <int DP, int SG, int THREADS>
+__global__ void __launch_bounds__(THREADS) merge_capture_kernel(const CaptureArgs c) {
+  constexpr int FC = DP / 4;
+  static_assert(THREADS == FC * SG, "one query vector per block");
+  __shared__ MergeRed<DP, SG> red;
+  const int tid = threadIdx.x, f = tid % FC, sg = tid / FC;
+  const int per_row = c.Hkv * c.T * c.G;
+  const int r = (int)blockIdx.x / per_row, local = (int)blockIdx.x - r * per_row;
+  const int qv_max = c.T * c.G;
+  const int h = local / qv_max, j = local - h * qv_max;
+  int count, length;
+  capture_row(c, r, count, length);
+  const int qrows = count * c.G;
+  const int nsplit = (length + c.tok_item - 1) / c.tok_item;
+  if (j >= qrows || nsplit <= 1) return;  // block-uniform
+  const int d = f * 4;
+  const int64_t ml_base = (int64_t)r * c.row_records + (int64_t)h * nsplit * qrows + j;
+  const int64_t ml_step = qrows;
+  const int g = j % c.G, i = j / c.G;
+  fold_and_write<DP, SG>(red, c.part_o, c.part_ml, ml_base * c.D + d, ml_step * c.D, ml_base, ml_step, nsplit,
+                         d < c.D, sg, f, c.out + r * c.o_sb + (int64_t)(h * c.G + g) * c.o_sh + (int64_t)i * c.o_st + d);
+}
+
+template <int DP>
+static hipError_t launch_merge_capture_d(const CaptureArgs &c, int max_splits, hipStream_t stream) {
+  constexpr int FC = DP / 4;
+  const dim3 grid(c.total_items);
+  if (max_splits <= 16 * (256 / FC))
+    hipLaunchKernelGGL((merge_capture_kernel<DP, 256 / FC, 256>), grid, dim3(256), 0, stream, c);
+  else if (max_splits <= 16 * (512 / FC))
+    hipLaunchKernelGGL((merge_capture_kernel<DP, 512 / FC, 512>), grid, dim3(512), 0, stream, c);
+  else
+    hipLaunchKernelGGL((merge_capture_kernel<DP, 1024 / FC, 1024>), grid, dim3(1024), 0, stream, c);
+  return hipGetLastError();
+}
+
+hipError_t launch_merge_capture(const CaptureArgs &c, int dp, int max_splits, hipStream_t stream) {
+  switch (dp) {
+    case 64: return launch_merge_capture_d<64>(c, max_splits, stream);
+    case 128: return launch_merge_capture_d<128>(c, max_splits, stream);
+    default: return launch_merge_capture_d<256>(c, max_splits, stream);
+  }
 }
 
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream) {

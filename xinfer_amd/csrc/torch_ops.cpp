@@ -135,6 +135,47 @@ at::Tensor batched_flash_attention_bthd(const at::Tensor &q, const at::Tensor &k
   return batched_attention(q, k, v, offsets, cuda_offsets, blocks, scale, true);
 }
 
+// Graph-capture variant of batched_flash_attention (decode batches): the same
+// schema, but the row lengths come from cuda_offsets when the kernels run;
+// the CPU offsets are checked for shape only, so a graph captured once stays
+// valid while the caller rewrites cuda_offsets (and the caches) in place
+// between replays.  Output and workspace shapes depend on the tensor shapes
+// only.
+at::Tensor batched_flash_attention_graph(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
+                                         const at::Tensor &offsets, const at::Tensor &cuda_offsets,
+                                         const at::Tensor &blocks, double scale) {
+  TORCH_CHECK(q.dim() == 4 && k.dim() == 4 && v.sizes() == k.sizes() && k.size(0) == q.size(0) &&
+                  k.size(3) == q.size(3),
+              "Invalid Q/K/V shapes");
+  TORCH_CHECK(q.is_cuda() && k.device() == q.device() && v.device() == q.device() &&
+                  q.scalar_type() == at::kBFloat16 && k.scalar_type() == q.scalar_type() &&
+                  v.scalar_type() == q.scalar_type(),
+              "Expected colocated CUDA BF16 Q/K/V");
+  const auto batch = q.size(0);
+  TORCH_CHECK(offsets.device().is_cpu() && offsets.scalar_type() == at::kInt &&
+                  offsets.sizes() == at::IntArrayRef({2, batch + 1}),
+              "Expected CPU int32 cumulative query/KV lengths [2,B+1]");
+  TORCH_CHECK(cuda_offsets.device() == q.device() && cuda_offsets.scalar_type() == at::kInt &&
+                  cuda_offsets.sizes() == offsets.sizes() && cuda_offsets.is_contiguous() &&
+                  blocks.device() == q.device() && blocks.scalar_type() == at::kInt &&
+                  blocks.sizes() == at::IntArrayRef({batch, 1}),
+              "Invalid CUDA attention metadata");
+  c10::DeviceGuard guard(q.device());
+  auto output = at::empty(q.sizes(), q.options());
+  if (batch == 0 || q.size(2) == 0) return output;
+  // Any row may read up to the capacity, so a layout copy covers all of it.
+  auto query = query_layout(q) ? q : q.contiguous();
+  auto key = kernel_layout(k) ? k : k.contiguous();
+  auto value = kernel_layout(v) ? v : v.contiguous();
+  auto qv = view_of(query), kv = view_of(key), vv = view_of(value);
+  const size_t bytes = xinfer_batched_flash_attention_graph_workspace_size(&qv, &kv);
+  auto workspace = at::empty({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
+  check_status(xinfer_batched_flash_attention_graph(&qv, &kv, &vv, static_cast<const int32_t *>(cuda_offsets.data_ptr()),
+                                                    scale, output.data_ptr(), workspace.data_ptr(), bytes,
+                                                    current_stream(q)));
+  return output;
+}
+
 // Replaces compiler/common/kernels/attention.cpp:82-124.
 at::Tensor flash_attention(const at::Tensor &q, const at::Tensor &k, const at::Tensor &v,
                            const at::Tensor &extent, double scale) {
@@ -288,6 +329,9 @@ TORCH_LIBRARY(xinfer, m) {
   m.def("batched_flash_attention_bthd(Tensor q, Tensor k, Tensor v, Tensor offsets, "
         "Tensor cuda_offsets, Tensor blocks, float scale) -> Tensor",
         {at::Tag::flexible_layout});
+  m.def("batched_flash_attention_graph(Tensor q, Tensor k, Tensor v, Tensor offsets, "
+        "Tensor cuda_offsets, Tensor blocks, float scale) -> Tensor",
+        {at::Tag::flexible_layout});
   m.def("append_kv_batched(Tensor key, Tensor value, Tensor positions, Tensor cu_query, "
         "Tensor(a4!) cache_key, Tensor(a5!) cache_value) -> ()");
   m.def("projection_gemv(Tensor x, Tensor weight) -> Tensor");
@@ -300,6 +344,7 @@ TORCH_LIBRARY_IMPL(xinfer, CUDA, m) {
   m.impl("batched_flash_attention", TORCH_FN(xinfer::batched_flash_attention));
   m.impl("flash_attention", TORCH_FN(xinfer::flash_attention));
   m.impl("batched_flash_attention_bthd", TORCH_FN(xinfer::batched_flash_attention_bthd));
+  m.impl("batched_flash_attention_graph", TORCH_FN(xinfer::batched_flash_attention_graph));
   m.impl("append_kv_batched", TORCH_FN(xinfer::append_kv_batched));
   m.impl("qk_norm_rope_append", TORCH_FN(xinfer::qk_norm_rope_append));
   m.impl("projection_gemv", TORCH_FN(xinfer::projection_gemv));
