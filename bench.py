@@ -50,7 +50,11 @@ BF16_PEAK_TFLOPS = 2516.6
 MALL_BYTES = 256 << 20
 METRIC = "decode attn KV GB/s (% HBM peak) + prefill TFLOP/s (% MFMA), bs 1–8 ragged"
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
-TRAFFIC_WORKLOADS = ("cfg2_prefill_b1_n512_p1536", "cfg3_ragged_decode_b8_seed0")
+# Workloads the traffic record's counter runs measure (``--only 2,3:0,4,5``):
+# each launches its own kernel instantiations, so per-kernel averages map to
+# one workload each.
+TRAFFIC_WORKLOADS = ("cfg2_prefill_b1_n512_p1536", "cfg3_ragged_decode_b8_seed0", "cfg4_decode_b4_d256",
+                     "cfg5_ragged_prefill_b8_seed0")
 KERNEL_SOURCES = ("xinfer_amd/csrc/*.hip", "xinfer_amd/csrc/*.h", "xinfer_amd/csrc/*.cpp")
 
 
@@ -127,9 +131,9 @@ def measured_traffic(w):
     """HBM bytes per launch of the dominant kernel from TRAFFIC_FILE, or None.
 
     None when no record exists, when it was taken on other kernel sources, or
-    for a workload other than the two the record's counter runs measure (the
-    default bench run: cfg2 and cfg3 seed 0); another workload launching the
-    same kernel moves other bytes.
+    for a workload other than those the record's counter runs measure
+    (TRAFFIC_WORKLOADS); another workload launching the same kernel moves
+    other bytes.
     """
     if w.name not in TRAFFIC_WORKLOADS:
         return None
@@ -638,6 +642,8 @@ def main():
                              "its JSON (cfg2 and cfg3 token shapes)")
     parser.add_argument("--gemv", action="store_true",
                         help="only time xinfer::projection_gemv against F.linear on the decoder geometries")
+    parser.add_argument("--only", default="",
+                        help="comma-separated workloads INDEX[:SEED] (e.g. 2,5,3:1) to time alone; prints their results")
     parser.add_argument("--graph-decode", action="store_true",
                         help="only time the graph-capture operator against the default one on the decode workloads")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -680,6 +686,17 @@ def main():
         print(json.dumps(measure_graph_decode(args.steps, args.warmup)), flush=True)
         return
     with_cpu = not args.no_cpu_baseline
+    if args.only:
+        picked = []
+        for item in args.only.split(","):
+            index, _, seed = item.partition(":")
+            picked.append(measure(int(index), int(seed or 0), args.steps, args.warmup, not args.eager, with_cpu,
+                                  args.cpu_budget))
+        print(json.dumps({r["workload"]: {"attention_op_us": round(r["attention_op_us"], 2),
+                                          "achieved": round(r["roofline"]["achieved"], 1), "unit": r["unit"],
+                                          "frac": round(r["roofline"]["frac"], 4),
+                                          "ms_per_step": r["ms_per_step"]} for r in picked}), flush=True)
+        return
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     extra = []
