@@ -21,10 +21,11 @@
 // buffer loads: the (row, head) base in scalar registers, a 32-bit lane offset
 // and a scalar per-row offset, so a load costs no vector address arithmetic;
 // the resource ends at the item's last key, and loads past it return zero
-// without touching memory.  Per block of U rows: bf16 dot2 against the lane's
-// 8 query features, a DPP all-reduce over the LPT lanes of a row, a block max
-// across the TPW row slots and an online-softmax update (running max m, sum l,
-// accumulator o), all lane-local.  The four waves are combined through LDS.
+// without touching memory.  Per key row: bf16 dot2 against the lane's 8 query
+// features and a DPP all-reduce over the LPT lanes of the row; then one max
+// over the wave's rows (all of them are in registers, so no online rescale),
+// and the fp32 weights and accumulation, all lane-local.  The four waves are
+// combined through LDS.
 //
 // One chunk per (row, head): the block writes normalised bf16 output.  Several
 // chunks: each writes an fp32 partial record per query vector, combined by
@@ -134,13 +135,15 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
   // anything); their query features are zero and their sums are not written.
   const uint32_t dcc = dc * 8 < a.D ? (uint32_t)dc : (uint32_t)(a.D / 8 - 1);
   const uint32_t vk = (uint32_t)first * row_bytes_k + dcc * 16, vv = (uint32_t)first * row_bytes_v + dcc * 16;
+  // Every K row before any V row: the scores need all of K, the weights none of V.
 #pragma unroll
-  for (int nb = 0; nb < S::NB; ++nb) {
+  for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
     for (int u = 0; u < S::U; ++u) r.k[nb][u] = buffer_load16_stream(rk, vk, (nb * S::BLK + u * S::TPW) * row_bytes_k);
 #pragma unroll
+  for (int nb = 0; nb < S::NB; ++nb)
+#pragma unroll
     for (int u = 0; u < S::U; ++u) r.v[nb][u] = buffer_load16_stream(rv, vv, (nb * S::BLK + u * S::TPW) * row_bytes_v);
-  }
 }
 
 template <int DP, int QR>
@@ -174,39 +177,39 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     if (!(j < qrows && dact)) r.q[j] = u32x4{0, 0, 0, 0};
   }
 
-  float m[QR], l[QR], acc[QR][8];
+  // The wave holds all of its keys of the item in registers, so its softmax
+  // needs no online rescale: every score first (masked to -inf), then the max
+  // m over the wave's keys (log2 units, the same on every lane), then the
+  // weights and the accumulation against that one max.
+  float sc[NB][QR][U], m[QR], l[QR], acc[QR][8];
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
-    m[j] = -INFINITY;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int tok = wb + nb * BLK + u * TPW + slot;
+        const float s = group_sum<LPT>(dot8_bf16(r.k[nb][u], r.q[j], 0.0f));
+        sc[nb][j][u] = (tok < we && tok <= lim[j]) ? s : -INFINITY;
+        mx = fmaxf(mx, sc[nb][j][u]);
+      }
+    m[j] = slot_max<LPT>(mx) * c;
     l[j] = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
   }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    float p[QR][U], alpha[QR];
+    float p[QR][U];
 #pragma unroll
     for (int j = 0; j < QR; ++j) {
-      float mb = -INFINITY;
+      const float mu = m[j] == -INFINITY ? 0.0f : m[j];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const int tok = wb + nb * BLK + u * TPW + slot;
-        const float s = group_sum<LPT>(dot8_bf16(r.k[nb][u], r.q[j], 0.0f));
-        p[j][u] = (tok < we && tok <= lim[j]) ? s : -INFINITY;
-        mb = fmaxf(mb, p[j][u]);
+        p[j][u] = fast_exp2(fmaf(sc[nb][j][u], c, -mu));
+        l[j] += p[j][u];
       }
-      mb = slot_max<LPT>(mb);
-      const float mn = fmaxf(m[j], mb * c);
-      const float mu = mn == -INFINITY ? 0.0f : mn;
-      alpha[j] = fast_exp2(m[j] - mu);
-      float ps = 0.0f;
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        p[j][u] = fast_exp2(fmaf(p[j][u], c, -mu));
-        ps += p[j][u];
-      }
-      l[j] = fmaf(l[j], alpha[j], ps);
-      m[j] = mn;
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -218,7 +221,7 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
       }
 #pragma unroll
       for (int j = 0; j < QR; ++j) {
-        float t = acc[j][e] * alpha[j];
+        float t = acc[j][e];
 #pragma unroll
         for (int u = 0; u < U; ++u) t = fmaf(p[j][u], vf[u], t);
         acc[j][e] = t;

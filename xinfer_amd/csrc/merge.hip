@@ -12,17 +12,20 @@
 // the records after the producing kernel has completed, which orders them
 // without any device-scope fence inside the attention kernels.
 //
-// A block is VPB query vectors x SG split lanes x FC feature lanes (4
-// features each): with few splits per vector (prefill) a 256-thread block has
-// SG = 1, one thread owning a vector's 4 features across all splits; with many
-// splits (long decode rows) one block per vector spreads them over SG =
-// THREADS / FC split lanes, THREADS (256, 512 or 1024) chosen so that a lane
-// loads at most one batch of 16 records.
+// With few splits per vector (prefill, short decode rows) a 256-thread block
+// holds VPB query vectors x FC feature lanes (4 features each), one thread
+// owning a vector's 4 features across all splits.  With many splits (long
+// decode rows) a block holds FS feature lanes of one vector and SG = THREADS /
+// FS split lanes: all FC feature lanes up to kMergeSliceSplits splits, past
+// that a slice of them, the FC / FS slices of a vector being separate blocks,
+// so a very long row's records are read by many CUs at once.  THREADS (256 to
+// 1024) is chosen so that a lane loads at most one batch of 16 records.
 //
-// Blocks are dealt to the 8 XCDs in contiguous runs of vectors (block b runs
-// vector group (b % 8) * (grid / 8) + b / 8), the order the prefill kernel
+// Blocks are dealt to the 8 XCDs in contiguous runs of work groups (block b
+// runs group (b % 8) * (grid / 8) + b / 8), the order the prefill kernel
 // gives its items, so the records a head's tiles wrote through one XCD's L2
-// are mostly read back on that XCD.
+// are mostly read back on that XCD, and a vector's slices share the (m, l)
+// reads in one L2.
 #include "device_common.h"
 #include "kernel_args.h"
 
@@ -48,18 +51,20 @@ __device__ __forceinline__ void fold(MergeState &st, float ms, float ls, f32x4 o
   st.m = mn;
 }
 
-template <int DP, int SG>
-using MergeRed = MergeState[SG > 1 ? SG : 1][SG > 1 ? DP / 4 : 1];
+// LDS states of a block with SG > 1 split lanes over FS feature lanes.
+template <int FS, int SG>
+using MergeRed = MergeState[SG > 1 ? SG : 1][SG > 1 ? FS : 1];
 
 // Folds the nsplit records of one query vector over this thread's 4 features
 // and writes them as bf16 at dst.  Record s: o at part_o + o_base + s * o_step,
 // (m, l) at part_ml + 2 * (ml_base + s * ml_step).  With SG > 1 split lanes
 // per feature group every thread of the block must call it (it synchronises
-// the block); `active` is false for threads past the vectors or features.
-// Every record of a batch is loaded before any is folded: a lane's splits take
+// the block); `active` is false for threads past the vectors or features, and
+// f is the thread's feature lane within the block's FS.  Every record of a
+// batch is loaded before any is folded: a lane's splits take
 // ceil(nsplit / (SG * INFLIGHT)) memory round trips.
-template <int DP, int SG>
-__device__ __forceinline__ void fold_and_write(MergeRed<DP, SG> &red, const float *part_o, const float *part_ml,
+template <int FS, int SG>
+__device__ __forceinline__ void fold_and_write(MergeRed<FS, SG> &red, const float *part_o, const float *part_ml,
                                                int64_t o_base, int64_t o_step, int64_t ml_base, int64_t ml_step,
                                                int nsplit, bool active, int sg, int f, uint16_t *dst) {
   constexpr int INFLIGHT = SG > 1 ? 16 : 4;
@@ -101,20 +106,20 @@ __device__ __forceinline__ void fold_and_write(MergeRed<DP, SG> &red, const floa
       u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
 }
 
-template <int DP, int SG, int THREADS>
+template <int DP, int SG, int THREADS, int FS>
 __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
-  constexpr int FC = DP / 4;                // feature lanes
-  constexpr int VPB = THREADS / (FC * SG);  // query vectors per block
-  __shared__ MergeRed<DP, SG> red;
+  constexpr int FC = DP / 4;                         // feature lanes of a vector
+  static_assert(SG == 1 ? FS == FC : FS * SG == THREADS, "block shape");
+  constexpr int NS = FC / FS;                        // feature slices per vector (SG > 1)
+  constexpr int VPB = SG > 1 ? 1 : THREADS / FC;     // query vectors per block
+  __shared__ MergeRed<FS, SG> red;
 
   // Few splits: vectors vary fastest across a block's threads (the prefill
   // record layout keeps a tile's vectors contiguous per feature group).
-  // Many splits: feature lanes vary fastest.
+  // Many splits: the slice's feature lanes vary fastest.
   const int tid = threadIdx.x;
-  const int f = SG > 1 ? tid % FC : tid / VPB, sg = SG > 1 ? (tid / FC) % SG : 0;
-  // With one vector per block the vector (and its row) is block-uniform, so
-  // the row lookup stays in scalar registers.
-  const int vl = VPB == 1 ? 0 : (SG > 1 ? tid / (FC * SG) : tid % VPB);
+  const int fl = SG > 1 ? tid % FS : tid / VPB, sg = SG > 1 ? tid / FS : 0;
+  const int vl = VPB == 1 ? 0 : tid % VPB;
   // Every argument of the block, loaded in one round trip (see XATTN_PIN_VIEW).
   RowLookup<MergeRow> rows;
   rows.load(a.rows);
@@ -125,10 +130,12 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   asm volatile(""
                : XATTN_PIN_BEGINS(rows), XATTN_PIN_MERGEROW(rows.first), "+s"(total_items), "+s"(nrows), "+s"(D),
                  "+s"(G), "+s"(out), "+s"(o_sb), "+s"(o_sh), "+s"(o_st), "+s"(part_o), "+s"(part_ml));
-  // The grid is the vector groups rounded up to a multiple of 8 (launch_merge_d).
-  const int groups = (total_items + VPB - 1) / VPB;
+  // Work groups: VPB vectors (few splits) or one slice of one vector.  The
+  // grid is the groups rounded up to a multiple of 8 (launch_merge_d).
+  const int groups = SG > 1 ? total_items * NS : (total_items + VPB - 1) / VPB;
   const int group = (int)(blockIdx.x % 8) * ((groups + 7) / 8) + (int)(blockIdx.x / 8);
-  const int vec = group * VPB + vl;
+  const int vec = SG > 1 ? group / NS : group * VPB + vl;
+  const int f = SG > 1 ? (group - vec * NS) * FS + fl : fl;  // feature lane of the vector
   const bool vvalid = vec < total_items;
   const MergeRow mr = rows.find(a.rows, nrows, vvalid ? vec : 0);
   const int local = vec - mr.item_begin;
@@ -153,31 +160,46 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   }
 
   const int g = j % G, i = j / G;
-  fold_and_write<DP, SG>(red, part_o, part_ml, o_base, o_step, ml_base, ml_step, mr.nsplit, vvalid && d < D, sg, f,
+  fold_and_write<FS, SG>(red, part_o, part_ml, o_base, o_step, ml_base, ml_step, mr.nsplit, vvalid && d < D, sg, fl,
                          out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st + d);
 }
 
 // Splits at or below this count use one thread per (vector, 4 features).
 constexpr int kMergeSerialSplits = 8;
 
+// Feature lanes per block past kMergeSliceSplits splits: 64 features, 256
+// contiguous bytes of each record.  Measured on MI355X: slicing takes cfg4's
+// 256-split merge (D = 256) from 10.3 to 7.2 us, and makes merges of 17 to 104
+// splits 0.2-0.8 us slower than one block per vector.
+constexpr int kMergeSliceLanes = 16;
+constexpr int kMergeSliceSplits = 128;
+
 template <int DP>
 static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t stream) {
   constexpr int FC = DP / 4;
-  // Grids are rounded up to a multiple of the 8 XCDs; surplus vectors exit.
+  // Grids are rounded up to a multiple of the 8 XCDs; surplus groups exit.
   if (max_splits <= kMergeSerialSplits) {
     constexpr int VPB = 256 / FC;
-    hipLaunchKernelGGL((merge_kernel<DP, 1, 256>), dim3(((a.total_items + VPB - 1) / VPB + 7) / 8 * 8), dim3(256), 0,
-                       stream, a);
-  } else {
+    hipLaunchKernelGGL((merge_kernel<DP, 1, 256, FC>), dim3(((a.total_items + VPB - 1) / VPB + 7) / 8 * 8), dim3(256),
+                       0, stream, a);
+  } else if (max_splits <= kMergeSliceSplits) {
     // One block per vector, with enough split lanes that each lane loads at
     // most one batch of 16 records when the block can grow to 1024 threads.
     const dim3 grid((a.total_items + 7) / 8 * 8);
     if (max_splits <= 16 * (256 / FC))
-      hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256>), grid, dim3(256), 0, stream, a);
+      hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256, FC>), grid, dim3(256), 0, stream, a);
     else if (max_splits <= 16 * (512 / FC))
-      hipLaunchKernelGGL((merge_kernel<DP, 512 / FC, 512>), grid, dim3(512), 0, stream, a);
+      hipLaunchKernelGGL((merge_kernel<DP, 512 / FC, 512, FC>), grid, dim3(512), 0, stream, a);
     else
-      hipLaunchKernelGGL((merge_kernel<DP, 1024 / FC, 1024>), grid, dim3(1024), 0, stream, a);
+      hipLaunchKernelGGL((merge_kernel<DP, 1024 / FC, 1024, FC>), grid, dim3(1024), 0, stream, a);
+  } else {
+    // One block per (vector, slice of FS feature lanes).
+    constexpr int FS = FC < kMergeSliceLanes ? FC : kMergeSliceLanes;
+    const dim3 grid(((int64_t)a.total_items * (FC / FS) + 7) / 8 * 8);
+    if (max_splits <= 16 * (256 / FS))
+      hipLaunchKernelGGL((merge_kernel<DP, 256 / FS, 256, FS>), grid, dim3(256), 0, stream, a);
+    else
+      hipLaunchKernelGGL((merge_kernel<DP, 512 / FS, 512, FS>), grid, dim3(512), 0, stream, a);
   }
   return hipGetLastError();
 }
@@ -191,7 +213,7 @@ template <int DP, int SG, int THREADS>
 __global__ void __launch_bounds__(THREADS) merge_capture_kernel(const CaptureArgs c) {
   constexpr int FC = DP / 4;
   static_assert(THREADS == FC * SG, "one query vector per block");
-  __shared__ MergeRed<DP, SG> red;
+  __shared__ MergeRed<FC, SG> red;
   const int tid = threadIdx.x, f = tid % FC, sg = tid / FC;
   const int per_row = c.Hkv * c.T * c.G;
   const int r = (int)blockIdx.x / per_row, local = (int)blockIdx.x - r * per_row;
@@ -206,7 +228,7 @@ __global__ void __launch_bounds__(THREADS) merge_capture_kernel(const CaptureArg
   const int64_t ml_base = (int64_t)r * c.row_records + (int64_t)h * nsplit * qrows + j;
   const int64_t ml_step = qrows;
   const int g = j % c.G, i = j / c.G;
-  fold_and_write<DP, SG>(red, c.part_o, c.part_ml, ml_base * c.D + d, ml_step * c.D, ml_base, ml_step, nsplit,
+  fold_and_write<FC, SG>(red, c.part_o, c.part_ml, ml_base * c.D + d, ml_step * c.D, ml_base, ml_step, nsplit,
                          d < c.D, sg, f, c.out + r * c.o_sb + (int64_t)(h * c.G + g) * c.o_sh + (int64_t)i * c.o_st + d);
 }
 
