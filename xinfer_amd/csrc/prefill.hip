@@ -9,12 +9,15 @@
 // vectors of one KV head are enumerated j = i*G + g (query i, grouped head g),
 // so one tile serves all G heads that share the K/V tile in LDS.
 //
-// Waves: four query groups of 32 vectors x KH key slices.  With KH = 2 (head
-// dims 64 and 128) a block is 8 waves, two per SIMD, so one wave's MFMAs
-// overlap the other's softmax; wave w+4 takes keys 32..63 of every 64-key
-// tile.  At the end waves w and w+4 exchange halves of their accumulators and
-// each finishes (and writes) half of the features.  Each wave computes the
-// transposed problem with v_mfma_f32_32x32x16_bf16:
+// Waves: four query groups of 32 vectors x KH.  With KH = 2 (head dims 64 and
+// 128) a block is 8 waves, two per SIMD, so one wave's MFMAs overlap the
+// other's softmax; waves w and w+4 (the same SIMD) take alternate 64-key tiles
+// of the item, each a whole tile, so a wave's per-tile softmax work (column
+// max, rescale test and rescale) is spent once per 64 keys and its two 32-key
+// score blocks are independent MFMA chains.  At the end waves w and w+4
+// exchange halves of their accumulators and each finishes (and writes) half of
+// the features.  Each wave computes the transposed problem with
+// v_mfma_f32_32x32x16_bf16:
 //   S^T[key, j]  = K[key, :] . Q[j, :]      A = K tile (LDS), B = Q^T (registers)
 //   O^T[d, j]   += V^T[d, key] P^T[key, j]  A = V^T (LDS, transposing reads), B = P^T
 // so a lane's accumulator column is one query vector: the online-softmax max /
@@ -145,7 +148,10 @@ struct PrefillShape {
   // 128 KB, else one tile per barrier over a ring of as many stages as fit.
   static constexpr int WIN = !QLDS && 4 * TILE * 4 <= 128 * 1024 ? 2 : 1;
   static constexpr int NST = WIN == 2 ? 4 : (QLDS ? (160 * 1024 - QBYTES) / (4 * TILE) : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2));
-  static constexpr int KPW = BN / KH;                 // keys of each tile per wave
+  // KH = 2: the two waves of a query group take alternate tiles (ALT), each
+  // all BN keys of its tile.
+  static constexpr bool ALT = KH > 1;
+  static constexpr int KPW = ALT ? BN : BN / KH;      // keys of a tile each wave computes
   static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
   static constexpr int HALF_T = KH > 1 ? NDT / 2 : NDT;  // d tiles each wave finishes
   static constexpr int FOLD = KH > 1 ? 8 * (HALF_T * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
@@ -282,9 +288,12 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   };
 
   // LDS read offsets (elements) of this lane, fixed for the whole item.
-  // K (A operand of QK): key kl = khalf*KPW + 32kt + col, chunk 2ds + half.
+  // K (A operand of QK): key kl = kbase + 32kt + col, chunk 2ds + half, with
+  // kbase the first key of the wave's share of a tile (0 when the waves of a
+  // query group alternate tiles).
   // Q (B operand, read once): row jr = qgroup*32 + col, same chunks.
-  const int kl0 = khalf * KPW + col, jr0 = qgroup * 32 + col;
+  const int kbase = S::ALT ? 0 : khalf * KPW;
+  const int kl0 = kbase + col, jr0 = qgroup * 32 + col;
   int k_off[NDS];
 #pragma unroll
   for (int ds = 0; ds < NDS; ++ds) k_off[ds] = kl0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(kl0)) * 8);
@@ -292,7 +301,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // addresses key kv0 (+16hh +8 for the second read) and features
   // 32t + 16(gq%2) + 4(jj%4); kv0 % 4 == jj / 4 for every read.
   const int gq = lane >> 4, jj = lane & 15;
-  const int kv0 = khalf * KPW + 4 * (gq >> 1) + (jj >> 2);
+  const int kv0 = kbase + 4 * (gq >> 1) + (jj >> 2);
   int v_off[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) {
@@ -311,7 +320,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   bf16x8 qf[NDS];  // Q^T B operands, read from LDS at tile 0
   auto compute = [&](int stage, int kb) {
     const uint16_t *Kt = smem + stage * 2 * TILE, *Vt = Kt + TILE;
-    const int kw = kb + khalf * KPW;  // first key of this wave's share
+    const int kw = kb + kbase;  // first key of this wave's share
     if (!(wave_active && kw <= wave_kmax && kw < ks1)) return;
     f32x16 s[NKT];
     if constexpr (S::QLDS) {
@@ -342,16 +351,19 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
+      // The NKT 32-key blocks are independent accumulation chains; k-step
+      // outer, so their MFMAs alternate.
 #pragma unroll
-      for (int kt = 0; kt < NKT; ++kt) {
+      for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
 #pragma unroll
-        for (int ds = 0; ds < NDS; ++ds) {
+      for (int ds = 0; ds < NDS; ++ds)
+#pragma unroll
+        for (int kt = 0; kt < NKT; ++kt) {
           const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
           s[kt] = mfma32(ka, qf[ds], s[kt]);
         }
-      }
     }
     // Mask keys past this column's causal limit or past the split.
     if (kw + KPW - 1 > wave_kmin || kw + KPW > ks1) {
@@ -457,8 +469,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     // Two-tile windows over four stages: at the start of the window of tiles
     // t, t+1 wait for their loads and synchronise (every wave is done with
     // tiles t-2 and t-1), refill those two stages with tiles t+2, t+3, then
-    // compute both tiles with no barrier between them, so the waves of a
-    // SIMD drift apart and overlap each other's MFMA, LDS and softmax phases.
+    // compute: waves 0-3 tile t, waves 4-7 tile t+1, with no barrier between
+    // the two, so the waves of a SIMD drift apart and overlap each other's
+    // MFMA, LDS and softmax phases.
     if (ntile > 0) {
       issue_query();
       issue(0, ks0);
@@ -473,8 +486,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
           if (t == 0) read_query();
           if (t + 2 < ntile) issue((2 * w + 2) % 4, ks0 + (t + 2) * BN);
           if (t + 3 < ntile) issue((2 * w + 3) % 4, ks0 + (t + 3) * BN);
-          compute(2 * w, ks0 + t * BN);
-          if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * BN);
+          static_assert(S::ALT, "two-tile windows: the waves of a query group alternate tiles");
+          if (khalf == 0) compute(2 * w, ks0 + t * BN);
+          else if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * BN);
         }
       }
     }
