@@ -160,13 +160,15 @@ struct PrefillShape {
 
 // XOR swizzles of the 16-byte chunks of a key row (chunk c of key k is stored
 // at slot c ^ swz(k)).  K: a K read takes chunk c of 32 consecutive keys, so
-// the 16 keys served together land in 16 different slots.  V: a transposing
-// read takes two adjacent chunks of 4 consecutive keys (k0 % 4 == 0), which
-// land in disjoint slot pairs.
+// the 16 keys served together land in 16 different slots.  V: the 32 lanes
+// one LDS pass serves (8 bytes each) read chunks 4t .. 4t+3 of 4 consecutive
+// keys (k0 % 4 == 0); the swizzle moves each key's four chunks to its own
+// group of four slots, i.e. its own 16 of the 64 banks.  (With D = 64 two
+// rows share the banks, so keys k and k+1 already differ in bank half.)
 template <int CHUNKS>
 __device__ __forceinline__ int k_swizzle(int key) { return key & (CHUNKS >= 16 ? 15 : CHUNKS - 1); }
 template <int CHUNKS>
-__device__ __forceinline__ int v_swizzle(int key) { return (2 * (key & 3)) & (CHUNKS - 1); }
+__device__ __forceinline__ int v_swizzle(int key) { return CHUNKS >= 16 ? 4 * (key & 3) : 4 * ((key >> 1) & 1); }
 
 template <int DP, int KH>
 __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
