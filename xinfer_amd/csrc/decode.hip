@@ -15,9 +15,10 @@
 // some blocks are in flight while others compute (measured on MI355X: 32 KB
 // per tensor per block is the read shape that sustains the most bandwidth).
 //
-// A block is 4 waves, each owning a contiguous quarter of the item.  LPT = D/8
-// lanes hold one key row (one 128-bit load per lane), so a wave instruction
-// reads TPW = 64/LPT whole rows (1 KB contiguous).  K and V are read with raw
+// A block is 4 waves, each owning a contiguous quarter of the item.  LPT lanes
+// hold one key row, CPL 16-byte chunks each (chunks dc, dc + LPT, ...), so a
+// wave instruction reads one 16-byte chunk of each lane, TPW = 64/LPT rows
+// (1 KB in runs of LPT*16 bytes).  K and V are read with raw
 // buffer loads: the (row, head) base in scalar registers, a 32-bit lane offset
 // and a scalar per-row offset, so a load costs no vector address arithmetic;
 // the resource ends at the item's last key, and loads past it return zero
@@ -43,12 +44,19 @@ namespace xattn {
 
 template <int DP, int QR>
 struct DecodeShape {
-  static constexpr int LPT = DP / 8;             // lanes per key row
+  // 16-byte chunks of a key row per lane.  Measured on MI355X: two chunks
+  // per lane for D = 256 (16 lanes per row, half the reduction steps per
+  // byte) lowers the occupancy of the four-query-vector kernel from 4 to 3
+  // waves per SIMD and is 2 us slower on a 122 MB decode batch.
+  static constexpr int CPL = 1;
+  static constexpr int LPT = DP / (8 * CPL);     // lanes per key row
   static constexpr int TPW = 64 / LPT;           // key rows per wave instruction
-  static constexpr int U = QR <= 2 ? 4 : (QR == 4 ? 2 : 1);  // rows per lane per block
-  // Blocks per wave per item: 16 KB of K+V per wave (8 KB for 8 query
+  // Key rows per lane per item: 16 KB of K+V per wave (8 KB for 8 query
   // vectors, whose accumulators take the registers).
-  static constexpr int NB = QR == 8 ? 4 : 8 / U;
+  static constexpr int ROWS = (QR == 8 ? 8 : 16) / (2 * CPL);
+  static constexpr int U0 = QR <= 2 ? 4 : (QR == 4 ? 2 : 1);
+  static constexpr int U = U0 < ROWS ? U0 : ROWS;  // rows per lane per block
+  static constexpr int NB = ROWS / U;            // blocks per wave per item
   static constexpr int BLK = TPW * U;            // keys per wave block
   static constexpr int TOK_WAVE = NB * BLK;      // keys per wave per item
   static constexpr int TOK_ITEM = 4 * TOK_WAVE;  // keys per work item
@@ -89,8 +97,17 @@ __device__ __forceinline__ DecodeItem locate_item(const RowSched &rs, int item, 
 template <int DP, int QR>
 struct DecodeRegs {
   using S = DecodeShape<DP, QR>;
-  u32x4 k[S::NB][S::U], v[S::NB][S::U], q[QR];
+  u32x4 k[S::NB][S::U][S::CPL], v[S::NB][S::U][S::CPL], q[QR][S::CPL];
 };
+
+// The c-th chunk of a key row this lane holds, clamped into the row (lanes
+// past D re-read the row's last chunk: bytes of the row itself, never the gap
+// after it, which a padded view may fill with anything).
+template <int DP, int QR>
+__device__ __forceinline__ int lane_chunk(int dc, int c, int D) {
+  const int chunk = dc + c * DecodeShape<DP, QR>::LPT;
+  return chunk * 8 < D ? chunk : D / 8 - 1;
+}
 
 // Zero out[b, h*G + g, t, :] for g < G and t in [t_begin, T).
 __device__ __forceinline__ void zero_queries(const DecodeParams &a, int b, int h, int t_begin) {
@@ -108,12 +125,12 @@ __device__ __forceinline__ void zero_queries(const DecodeParams &a, int b, int h
 template <int DP, int QR>
 __device__ __forceinline__ void load_query(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r, int dc) {
   const int qrows = it.cnt * a.G;
-  const int dcc = dc * 8 < a.D ? dc : a.D / 8 - 1;
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
     const int jc = j < qrows ? j : qrows - 1;
-    r.q[j] = load16(a.q.p + it.b * a.q.sb + (int64_t)(it.h * a.G + jc % a.G) * a.q.sh +
-                    (int64_t)(jc / a.G) * a.q.st + dcc * 8);
+    const uint16_t *qrow = a.q.p + it.b * a.q.sb + (int64_t)(it.h * a.G + jc % a.G) * a.q.sh + (int64_t)(jc / a.G) * a.q.st;
+#pragma unroll
+    for (int c = 0; c < DecodeShape<DP, QR>::CPL; ++c) r.q[j][c] = load16(qrow + lane_chunk<DP, QR>(dc, c, a.D) * 8);
   }
 }
 
@@ -130,20 +147,30 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
   const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
   const auto rv = buffer_rsrc(a.v.p + it.b * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
   const int first = it.t0 + wave * S::TOK_WAVE + slot;  // this lane's first key row
-  // Lanes past D (padded head dims) re-read the row's last chunk: bytes of the
-  // row itself, never the gap after it (which a padded view may fill with
-  // anything); their query features are zero and their sums are not written.
-  const uint32_t dcc = dc * 8 < a.D ? (uint32_t)dc : (uint32_t)(a.D / 8 - 1);
-  const uint32_t vk = (uint32_t)first * row_bytes_k + dcc * 16, vv = (uint32_t)first * row_bytes_v + dcc * 16;
+  // Chunks past D (padded head dims) are clamped into the row; their query
+  // features are zero and their sums are not written.
+  uint32_t vk[S::CPL], vv[S::CPL];
+#pragma unroll
+  for (int c = 0; c < S::CPL; ++c) {
+    const uint32_t chunk = (uint32_t)lane_chunk<DP, QR>(dc, c, a.D);
+    vk[c] = (uint32_t)first * row_bytes_k + chunk * 16;
+    vv[c] = (uint32_t)first * row_bytes_v + chunk * 16;
+  }
   // Every K row before any V row: the scores need all of K, the weights none of V.
 #pragma unroll
   for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
-    for (int u = 0; u < S::U; ++u) r.k[nb][u] = buffer_load16_stream(rk, vk, (nb * S::BLK + u * S::TPW) * row_bytes_k);
+    for (int u = 0; u < S::U; ++u)
+#pragma unroll
+      for (int c = 0; c < S::CPL; ++c)
+        r.k[nb][u][c] = buffer_load16_stream(rk, vk[c], (nb * S::BLK + u * S::TPW) * row_bytes_k);
 #pragma unroll
   for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
-    for (int u = 0; u < S::U; ++u) r.v[nb][u] = buffer_load16_stream(rv, vv, (nb * S::BLK + u * S::TPW) * row_bytes_v);
+    for (int u = 0; u < S::U; ++u)
+#pragma unroll
+      for (int c = 0; c < S::CPL; ++c)
+        r.v[nb][u][c] = buffer_load16_stream(rv, vv[c], (nb * S::BLK + u * S::TPW) * row_bytes_v);
 }
 
 template <int DP, int QR>
@@ -157,7 +184,8 @@ template <int DP, int QR>
 __device__ __forceinline__ void process_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
                                              DecodeShared<DP, QR> &sh, int wave, int lane, int slot, int dc) {
   using S = DecodeShape<DP, QR>;
-  constexpr int LPT = S::LPT, TPW = S::TPW, U = S::U, NB = S::NB, BLK = S::BLK;
+  constexpr int LPT = S::LPT, TPW = S::TPW, U = S::U, NB = S::NB, BLK = S::BLK, CPL = S::CPL;
+  constexpr int F = 8 * CPL;  // output features per lane
   const int tid = threadIdx.x, G = a.G;
   if (it.cnt == 0) {
     zero_queries(a, it.b, it.h, 0);
@@ -169,35 +197,60 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
   const float c = a.scale_log2;
   const int wb = it.t0 + wave * S::TOK_WAVE;
   const int we = min(it.t1, wb + S::TOK_WAVE);
-  const bool dact = dc * 8 < a.D;
   int lim[QR];
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
     lim[j] = j < qrows ? it.L - it.cnt + j / G : -1;  // last visible key of query vector j
-    if (!(j < qrows && dact)) r.q[j] = u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc)
+      if (!(j < qrows && (dc + cc * LPT) * 8 < a.D)) r.q[j][cc] = u32x4{0, 0, 0, 0};
   }
+  // Keys need masking only in a wave whose rows reach past the item (the
+  // row's end) or past the first query's causal limit, L - count; query
+  // vectors past qrows are never written.  The test is wave-uniform.
+  const bool masked = wb + S::TOK_WAVE > we || wb + S::TOK_WAVE - 1 > it.L - it.cnt;
 
   // The wave holds all of its keys of the item in registers, so its softmax
   // needs no online rescale: every score first (masked to -inf), then the max
   // m over the wave's keys (log2 units, the same on every lane), then the
   // weights and the accumulation against that one max.
-  float sc[NB][QR][U], m[QR], l[QR], acc[QR][8];
+  float sc[NB][QR][U], m[QR], l[QR], acc[QR][F];
+  auto score = [&](int nb, int j, int u) {
+    float d = 0.0f;
+#pragma unroll
+    for (int cc = 0; cc < CPL; ++cc) d = dot8_bf16(r.k[nb][u][cc], r.q[j][cc], d);
+    return group_sum<LPT>(d);
+  };
+  if (masked) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int j = 0; j < QR; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const int tok = wb + nb * BLK + u * TPW + slot;
+          const float sv = score(nb, j, u);
+          sc[nb][j][u] = (tok < we && tok <= lim[j]) ? sv : -INFINITY;
+        }
+  } else {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int j = 0; j < QR; ++j)
+#pragma unroll
+        for (int u = 0; u < U; ++u) sc[nb][j][u] = score(nb, j, u);
+  }
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
     float mx = -INFINITY;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int tok = wb + nb * BLK + u * TPW + slot;
-        const float s = group_sum<LPT>(dot8_bf16(r.k[nb][u], r.q[j], 0.0f));
-        sc[nb][j][u] = (tok < we && tok <= lim[j]) ? s : -INFINITY;
-        mx = fmaxf(mx, sc[nb][j][u]);
-      }
+      for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[nb][j][u]);
     m[j] = slot_max<LPT>(mx) * c;
     l[j] = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = 0.0f;
+    for (int e = 0; e < F; ++e) acc[j][e] = 0.0f;
   }
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
@@ -212,11 +265,11 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
       }
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
+    for (int e = 0; e < F; ++e) {
       float vf[U];
 #pragma unroll
       for (int u = 0; u < U; ++u) {
-        const uint32_t w = r.v[nb][u][e >> 1];
+        const uint32_t w = r.v[nb][u][e / 8][(e % 8) >> 1];
         vf[u] = (e & 1) ? bf16_hi(w) : bf16_lo(w);
       }
 #pragma unroll
@@ -234,13 +287,17 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
   for (int j = 0; j < QR; ++j) {
     l[j] = slot_sum<LPT>(l[j]);
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[j][e] = slot_sum<LPT>(acc[j][e]);
+    for (int e = 0; e < F; ++e) acc[j][e] = slot_sum<LPT>(acc[j][e]);
   }
-  if (slot == 0 && dact) {
+  if (slot == 0) {
 #pragma unroll
-    for (int j = 0; j < QR; ++j)
+    for (int cc = 0; cc < CPL; ++cc)
+      if ((dc + cc * LPT) * 8 < a.D) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) sh.red_o[wave][j][dc * 8 + e] = acc[j][e];
+        for (int j = 0; j < QR; ++j)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) sh.red_o[wave][j][(dc + cc * LPT) * 8 + e] = acc[j][cc * 8 + e];
+      }
   }
   if (lane == 0) {
 #pragma unroll
@@ -372,8 +429,15 @@ hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int block
 }
 
 int decode_tokens_per_item(int dp, int qr) {
-  const int u = qr <= 2 ? 4 : (qr == 4 ? 2 : 1);
-  return 4 * (qr == 8 ? 4 : 8 / u) * (64 / (dp / 8)) * u;
+  switch (dp * 16 + qr) {
+#define XATTN_TOK(D, Q) \
+  case D * 16 + Q: return DecodeShape<D, Q>::TOK_ITEM;
+    XATTN_TOK(64, 1) XATTN_TOK(64, 2) XATTN_TOK(64, 4) XATTN_TOK(64, 8)
+    XATTN_TOK(128, 1) XATTN_TOK(128, 2) XATTN_TOK(128, 4) XATTN_TOK(128, 8)
+    XATTN_TOK(256, 1) XATTN_TOK(256, 2) XATTN_TOK(256, 4) XATTN_TOK(256, 8)
+#undef XATTN_TOK
+    default: return 0;
+  }
 }
 
 template <int DP>
