@@ -527,8 +527,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
 
   // Per-lane partial sum -> column sum (lanes l and l^32 hold the two key halves of a 32x32 tile).
   l_run = pair_sum32(l_run);
-  // Fold of the two key slices.  Waves w and w+4 hold the same 32 query
-  // vectors; wave w finishes d tiles 0 .. NDT/2-1 and wave w+4 the others:
+  // Fold of the two waves' states.  Waves w and w+4 hold the same 32 query
+  // vectors over alternate tiles; wave w finishes d tiles 0 .. NDT/2-1 and
+  // wave w+4 the others:
   // each hands the other's half of its accumulator, and its (m, l), through
   // LDS, combines the half it keeps and writes that half of the output.
   constexpr int HALF_T = S::HALF_T;
