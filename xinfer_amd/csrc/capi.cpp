@@ -21,6 +21,7 @@ namespace xattn {
 namespace {
 
 constexpr int kDecodeMaxQueryVectors = 8;  // G * count at or below this: decode kernel
+constexpr int64_t kDecodeTwoRoundItems = 1536;  // one-round decode items from which items take two rounds
 constexpr int kPrefillTileQ = 128;         // query vectors per prefill work item
 constexpr int64_t kPrefillMinSplitKeys = 512;
 
@@ -65,7 +66,7 @@ int check_heads_and_dim(const Geometry &g) {
 struct Group {
   int row0 = 0, nrows = 0;
   AttnArgs dec{};
-  int dec_items = 0, dec_qr = 1;
+  int dec_items = 0, dec_qr = 1, dec_rounds = 1;
   AttnArgs pre{};
   int pre_items = 0;
   MergeArgs merge{};
@@ -214,7 +215,17 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
       if (qv > 0 && qv <= kDecodeMaxQueryVectors) max_qv = std::max(max_qv, qv);
     }
     grp.dec_qr = pow2_at_least(max_qv);
-    const int tpi = decode_tokens_per_item(dp, grp.dec_qr);
+    // Two rounds per decode item when one-round items would give at least
+    // kDecodeTwoRoundItems blocks: fewer, longer items halve the split
+    // records; small batches keep one round for the parallelism.
+    int64_t one_round_items = 0;
+    for (int r = 0; r < grp.nrows; ++r) {
+      const int64_t qv = (int64_t)counts[row0 + r] * G;
+      if (qv > 0 && qv <= kDecodeMaxQueryVectors)
+        one_round_items += g.Hkv * ceil_div(lengths[row0 + r], decode_tokens_per_item(dp, grp.dec_qr));
+    }
+    grp.dec_rounds = one_round_items >= kDecodeTwoRoundItems ? 2 : 1;
+    const int tpi = grp.dec_rounds * decode_tokens_per_item(dp, grp.dec_qr);
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t b = row0 + r;
       const int cnt = counts[b], len = lengths[b];
@@ -286,7 +297,7 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
     }
     grp.dec.total_items = grp.dec_items;
     grp.pre.total_items = grp.pre_items;
-    if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_items, stream) != hipSuccess)
+    if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_rounds, grp.dec_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
     if (grp.pre_items > 0) {
       xcd_runs(prefill_item_work(grp.pre.rows, grp.pre.nrows, g.Hkv, G, dp), grp.pre.xcd_begin);

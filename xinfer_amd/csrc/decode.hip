@@ -58,9 +58,16 @@ struct DecodeShape {
   static constexpr int U = U0 < ROWS ? U0 : ROWS;  // rows per lane per block
   static constexpr int NB = ROWS / U;            // blocks per wave per item
   static constexpr int BLK = TPW * U;            // keys per wave block
-  static constexpr int TOK_WAVE = NB * BLK;      // keys per wave per item
-  static constexpr int TOK_ITEM = 4 * TOK_WAVE;  // keys per work item
+  static constexpr int TOK_WAVE = NB * BLK;      // keys per wave per round
+  static constexpr int TOK_ROUND = 4 * TOK_WAVE; // keys per block per round
 };
+
+// An item takes ROUNDS rounds: the block loads and computes TOK_ROUND keys at
+// a time, reusing the registers, and writes one output or record per item.
+// The planner takes two rounds for launches that have many items (measured on
+// MI355X: 2 us faster on a 122 MB D = 256 batch, neutral on the 126 MB D = 128
+// one, and slower on small batches, which then have too few blocks).
+constexpr int kDecodeMaxRounds = 2;
 
 struct DecodeItem {
   int b, h, split, nsplit, cnt, L, t0, t1;
@@ -134,19 +141,22 @@ __device__ __forceinline__ void load_query(const DecodeParams &a, const DecodeIt
   }
 }
 
-// Issue every load of an item: K/V rows through buffer resources ending at the
-// item's last key, and the query features (clamped into the row, zeroed past D).
+// Issue every load of one round of an item: K/V rows through buffer resources
+// ending at the item's last key, and (round 0) the query features (clamped
+// into the row, zeroed past D).
 template <int DP, int QR>
 __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
-                                           int wave, int slot, int dc) {
+                                           int wave, int slot, int dc, int round = 0) {
   using S = DecodeShape<DP, QR>;
   if (it.cnt == 0) return;
   // The query first: its loads complete before the K/V rows the first dot needs.
-  if constexpr (QR <= 4) load_query(a, it, r, dc);  // wider groups load it in process_item
+  if constexpr (QR <= 4) {
+    if (round == 0) load_query(a, it, r, dc);  // wider groups load it in process_item
+  }
   const uint32_t row_bytes_k = (uint32_t)(a.k.st * 2), row_bytes_v = (uint32_t)(a.v.st * 2);
   const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
   const auto rv = buffer_rsrc(a.v.p + it.b * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
-  const int first = it.t0 + wave * S::TOK_WAVE + slot;  // this lane's first key row
+  const int first = it.t0 + round * S::TOK_ROUND + wave * S::TOK_WAVE + slot;  // this lane's first key row
   // Chunks past D (padded head dims) are clamped into the row; their query
   // features are zero and their sums are not written.
   uint32_t vk[S::CPL], vv[S::CPL];
@@ -179,8 +189,9 @@ struct DecodeShared {
   float red_m[4][QR], red_l[4][QR];
 };
 
-// Compute one item from its registers; writes output or partial records.
-template <int DP, int QR>
+// Compute one item from its registers (round 0 already issued); writes output
+// or partial records.
+template <int DP, int QR, int ROUNDS>
 __device__ __forceinline__ void process_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
                                              DecodeShared<DP, QR> &sh, int wave, int lane, int slot, int dc) {
   using S = DecodeShape<DP, QR>;
@@ -195,8 +206,6 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
   if constexpr (QR > 4) load_query(a, it, r, dc);
   const int qrows = it.cnt * G;
   const float c = a.scale_log2;
-  const int wb = it.t0 + wave * S::TOK_WAVE;
-  const int we = min(it.t1, wb + S::TOK_WAVE);
   int lim[QR];
 #pragma unroll
   for (int j = 0; j < QR; ++j) {
@@ -205,15 +214,12 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     for (int cc = 0; cc < CPL; ++cc)
       if (!(j < qrows && (dc + cc * LPT) * 8 < a.D)) r.q[j][cc] = u32x4{0, 0, 0, 0};
   }
-  // Keys need masking only in a wave whose rows reach past the item (the
-  // row's end) or past the first query's causal limit, L - count; query
-  // vectors past qrows are never written.  The test is wave-uniform.
-  const bool masked = wb + S::TOK_WAVE > we || wb + S::TOK_WAVE - 1 > it.L - it.cnt;
 
-  // The wave holds all of its keys of the item in registers, so its softmax
-  // needs no online rescale: every score first (masked to -inf), then the max
-  // m over the wave's keys (log2 units, the same on every lane), then the
-  // weights and the accumulation against that one max.
+  // A round's keys are all in registers, so within a round the softmax needs
+  // no online rescale: every score first (masked to -inf), then the max over
+  // the wave's keys of the round (log2 units, the same on every lane), then
+  // the weights and the accumulation against the running max m, which the
+  // round's max may raise once (one rescale of the accumulators per round).
   float sc[NB][QR][U], m[QR], l[QR], acc[QR][F];
   auto score = [&](int nb, int j, int u) {
     float d = 0.0f;
@@ -221,63 +227,86 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     for (int cc = 0; cc < CPL; ++cc) d = dot8_bf16(r.k[nb][u][cc], r.q[j][cc], d);
     return group_sum<LPT>(d);
   };
-  if (masked) {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+  for (int round = 0; round < ROUNDS; ++round) {
+    if (round > 0) {
+      if (it.t0 + round * S::TOK_ROUND >= it.t1) break;  // block-uniform: the item ends earlier
+      issue_item(a, it, r, wave, slot, dc, round);
+    }
+    const int wb = it.t0 + round * S::TOK_ROUND + wave * S::TOK_WAVE;
+    const int we = min(it.t1, wb + S::TOK_WAVE);
+    // Keys need masking only in a wave whose rows reach past the item (the
+    // row's end) or past the first query's causal limit, L - count; query
+    // vectors past qrows are never written.  The test is wave-uniform.
+    const bool masked = wb + S::TOK_WAVE > we || wb + S::TOK_WAVE - 1 > it.L - it.cnt;
+    if (masked) {
 #pragma unroll
-      for (int j = 0; j < QR; ++j)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const int tok = wb + nb * BLK + u * TPW + slot;
-          const float sv = score(nb, j, u);
-          sc[nb][j][u] = (tok < we && tok <= lim[j]) ? sv : -INFINITY;
-        }
-  } else {
+        for (int j = 0; j < QR; ++j)
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
+          for (int u = 0; u < U; ++u) {
+            const int tok = wb + nb * BLK + u * TPW + slot;
+            const float sv = score(nb, j, u);
+            sc[nb][j][u] = (tok < we && tok <= lim[j]) ? sv : -INFINITY;
+          }
+    } else {
 #pragma unroll
-      for (int j = 0; j < QR; ++j)
+      for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-        for (int u = 0; u < U; ++u) sc[nb][j][u] = score(nb, j, u);
-  }
+        for (int j = 0; j < QR; ++j)
 #pragma unroll
-  for (int j = 0; j < QR; ++j) {
-    float mx = -INFINITY;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[nb][j][u]);
-    m[j] = slot_max<LPT>(mx) * c;
-    l[j] = 0.0f;
-#pragma unroll
-    for (int e = 0; e < F; ++e) acc[j][e] = 0.0f;
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    float p[QR][U];
+          for (int u = 0; u < U; ++u) sc[nb][j][u] = score(nb, j, u);
+    }
 #pragma unroll
     for (int j = 0; j < QR; ++j) {
-      const float mu = m[j] == -INFINITY ? 0.0f : m[j];
+      float mx = -INFINITY;
 #pragma unroll
-      for (int u = 0; u < U; ++u) {
-        p[j][u] = fast_exp2(fmaf(sc[nb][j][u], c, -mu));
-        l[j] += p[j][u];
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int u = 0; u < U; ++u) mx = fmaxf(mx, sc[nb][j][u]);
+      const float mt = slot_max<LPT>(mx) * c;
+      if (round == 0) {
+        m[j] = mt;
+        l[j] = 0.0f;
+#pragma unroll
+        for (int e = 0; e < F; ++e) acc[j][e] = 0.0f;
+      } else {
+        const float m_new = fmaxf(m[j], mt);
+        const float alpha = fast_exp2(m[j] - (m_new == -INFINITY ? 0.0f : m_new));  // m = -inf: 0
+        l[j] *= alpha;
+#pragma unroll
+        for (int e = 0; e < F; ++e) acc[j][e] *= alpha;
+        m[j] = m_new;
       }
     }
 #pragma unroll
-    for (int e = 0; e < F; ++e) {
-      float vf[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const uint32_t w = r.v[nb][u][e / 8][(e % 8) >> 1];
-        vf[u] = (e & 1) ? bf16_hi(w) : bf16_lo(w);
-      }
+    for (int nb = 0; nb < NB; ++nb) {
+      float p[QR][U];
 #pragma unroll
       for (int j = 0; j < QR; ++j) {
-        float t = acc[j][e];
+        const float mu = m[j] == -INFINITY ? 0.0f : m[j];
 #pragma unroll
-        for (int u = 0; u < U; ++u) t = fmaf(p[j][u], vf[u], t);
-        acc[j][e] = t;
+        for (int u = 0; u < U; ++u) {
+          p[j][u] = fast_exp2(fmaf(sc[nb][j][u], c, -mu));
+          l[j] += p[j][u];
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < F; ++e) {
+        float vf[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const uint32_t w = r.v[nb][u][e / 8][(e % 8) >> 1];
+          vf[u] = (e & 1) ? bf16_hi(w) : bf16_lo(w);
+        }
+#pragma unroll
+        for (int j = 0; j < QR; ++j) {
+          float t = acc[j][e];
+#pragma unroll
+          for (int u = 0; u < U; ++u) t = fmaf(p[j][u], vf[u], t);
+          acc[j][e] = t;
+        }
       }
     }
   }
@@ -336,7 +365,7 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
   }
 }
 
-template <int DP, int QR>
+template <int DP, int QR, int ROUNDS>
 __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   using S = DecodeShape<DP, QR>;
   __shared__ DecodeShared<DP, QR> sh;
@@ -352,10 +381,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
                  XATTN_PIN_VIEW(p.k), XATTN_PIN_VIEW(p.v), "+s"(p.out), "+s"(p.o_sb), "+s"(p.o_sh), "+s"(p.o_st),
                  "+s"(p.part_o), "+s"(p.part_ml), "+s"(p.scale_log2), "+s"(p.D), "+s"(p.G), "+s"(p.T));
   const int item = blockIdx.x;
-  const DecodeItem it = locate_item(rows.find(a.rows, nrows, item), item, S::TOK_ITEM);
+  const DecodeItem it = locate_item(rows.find(a.rows, nrows, item), item, ROUNDS * S::TOK_ROUND);
   DecodeRegs<DP, QR> r;
   issue_item(p, it, r, wave, slot, dc);
-  process_item(p, it, r, sh, wave, lane, slot, dc);
+  process_item<DP, QR, ROUNDS>(p, it, r, sh, wave, lane, slot, dc);
 }
 
 // Graph-capture decode: the launch shape depends only on the tensor shapes.
@@ -401,10 +430,10 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
     rs.nsplit = row_splits[r];
     rs.ntiles = 1;
     rs.rec_begin = (int64_t)r * c.row_records;
-    const DecodeItem it = locate_item(rs, item, S::TOK_ITEM);
+    const DecodeItem it = locate_item(rs, item, S::TOK_ROUND);
     DecodeRegs<DP, QR> regs;
     issue_item(p, it, regs, wave, slot, dc);
-    process_item(p, it, regs, sh, wave, lane, slot, dc);
+    process_item<DP, QR, 1>(p, it, regs, sh, wave, lane, slot, dc);
     __syncthreads();  // the next item reuses the block's reduction buffers
   }
 }
@@ -431,7 +460,7 @@ hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int block
 int decode_tokens_per_item(int dp, int qr) {
   switch (dp * 16 + qr) {
 #define XATTN_TOK(D, Q) \
-  case D * 16 + Q: return DecodeShape<D, Q>::TOK_ITEM;
+  case D * 16 + Q: return DecodeShape<D, Q>::TOK_ROUND;
     XATTN_TOK(64, 1) XATTN_TOK(64, 2) XATTN_TOK(64, 4) XATTN_TOK(64, 8)
     XATTN_TOK(128, 1) XATTN_TOK(128, 2) XATTN_TOK(128, 4) XATTN_TOK(128, 8)
     XATTN_TOK(256, 1) XATTN_TOK(256, 2) XATTN_TOK(256, 4) XATTN_TOK(256, 8)
@@ -440,22 +469,28 @@ int decode_tokens_per_item(int dp, int qr) {
   }
 }
 
-template <int DP>
-static hipError_t launch_decode_d(const AttnArgs &a, int qr, int blocks, hipStream_t stream) {
+template <int DP, int ROUNDS>
+static hipError_t launch_decode_r(const AttnArgs &a, int qr, int blocks, hipStream_t stream) {
   switch (qr) {
-    case 1: hipLaunchKernelGGL((decode_kernel<DP, 1>), dim3(blocks), dim3(256), 0, stream, a); break;
-    case 2: hipLaunchKernelGGL((decode_kernel<DP, 2>), dim3(blocks), dim3(256), 0, stream, a); break;
-    case 4: hipLaunchKernelGGL((decode_kernel<DP, 4>), dim3(blocks), dim3(256), 0, stream, a); break;
-    default: hipLaunchKernelGGL((decode_kernel<DP, 8>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 1: hipLaunchKernelGGL((decode_kernel<DP, 1, ROUNDS>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((decode_kernel<DP, 2, ROUNDS>), dim3(blocks), dim3(256), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((decode_kernel<DP, 4, ROUNDS>), dim3(blocks), dim3(256), 0, stream, a); break;
+    default: hipLaunchKernelGGL((decode_kernel<DP, 8, ROUNDS>), dim3(blocks), dim3(256), 0, stream, a); break;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int blocks, hipStream_t stream) {
+template <int DP>
+static hipError_t launch_decode_d(const AttnArgs &a, int qr, int rounds, int blocks, hipStream_t stream) {
+  static_assert(kDecodeMaxRounds == 2, "rounds dispatch");
+  return rounds == 2 ? launch_decode_r<DP, 2>(a, qr, blocks, stream) : launch_decode_r<DP, 1>(a, qr, blocks, stream);
+}
+
+hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int blocks, hipStream_t stream) {
   switch (dp) {
-    case 64: return launch_decode_d<64>(a, qr, blocks, stream);
-    case 128: return launch_decode_d<128>(a, qr, blocks, stream);
-    default: return launch_decode_d<256>(a, qr, blocks, stream);
+    case 64: return launch_decode_d<64>(a, qr, rounds, blocks, stream);
+    case 128: return launch_decode_d<128>(a, qr, rounds, blocks, stream);
+    default: return launch_decode_d<256>(a, qr, rounds, blocks, stream);
   }
 }
 

@@ -12,10 +12,11 @@ hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t stream);
 // fp32: float inputs and output, else bf16; vec: 16-byte aligned rows and input.
 hipError_t launch_gemv(const GemvArgs &a, bool fp32, bool vec, hipStream_t stream);
 
-// Keys handled by one decode work item for padded head dim `dp` and `qr` query
-// vectors per KV head (a power of two <= 8).
+// Keys of one decode round for padded head dim `dp` and `qr` query vectors per
+// KV head (a power of two <= 8); an item of `rounds` rounds (1 or 2) takes
+// rounds times as many.
 int decode_tokens_per_item(int dp, int qr);
-hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int items, hipStream_t stream);
+hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int items, hipStream_t stream);
 
 hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream);
 
