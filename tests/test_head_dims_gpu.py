@@ -8,7 +8,7 @@ the output row's.  Each case checks against the float64 oracle:
 
 * decode rows (G * count <= 8 query vectors per KV head) with one item, with
   a few splits (the one-thread-per-vector merge), with many splits (the
-  split-lane merge) and with more than 128 (the feature-sliced merge);
+  split-lane merge) and with more than 64 (the feature-sliced merge);
 * prefill rows with and without key splits, and a row with G = 1;
 * K/V/Q stored as views of wider rows whose gap holds NaN, so a read past D
   poisons the output.
@@ -31,10 +31,10 @@ CASES = (
     ("decode_one_item", 8, 4, [1, 1, 1], [1, 37, 100], 128),
     ("decode_few_splits", 8, 4, [1, 2, 1], [700, 300, 1], 1024),
     ("decode_many_splits", 8, 4, [1, 1], [3000, 57], 3072),
-    # Past 128 splits the merge cuts a vector's features into blocks of 64
-    # (and past 256 splits, 512-thread blocks): 266 splits at padded dim 256,
-    # 133 at 128, 67 (one block per vector) at 64.
-    ("decode_sliced_merge", 8, 4, [1, 1], [17000, 70], 17024),
+    # Past 64 splits the merge cuts a vector's features into blocks of 64
+    # (and past 256 splits, 512-thread blocks): 258 splits at padded dims 256
+    # (two-round items) and 128, 129 at 64.
+    ("decode_sliced_merge", 8, 4, [1, 1], [33000, 70], 33024),
     ("decode_group1", 4, 4, [1, 4], [900, 200], 1024),
     ("prefill_unsplit", 8, 4, [100, 1], [300, 64], 512),
     ("prefill_split", 8, 4, [200, 64, 0], [2100, 1500, 9], 2176),

@@ -168,11 +168,12 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
 constexpr int kMergeSerialSplits = 8;
 
 // Feature lanes per block past kMergeSliceSplits splits: 64 features, 256
-// contiguous bytes of each record.  Measured on MI355X: slicing takes cfg4's
-// 256-split merge (D = 256) from 10.3 to 7.2 us, and makes merges of 17 to 104
-// splits 0.2-0.8 us slower than one block per vector.
+// contiguous bytes of each record.  Measured on MI355X: slicing takes a
+// 16384-key D = 256 row's merge from 10.3 to 7.2 us at 256 splits and from
+// 6.5 to 5.9 us at 128, and makes merges of 17 to 52 splits 0.2-0.8 us
+// slower than one block per vector.
 constexpr int kMergeSliceLanes = 16;
-constexpr int kMergeSliceSplits = 128;
+constexpr int kMergeSliceSplits = 64;
 
 template <int DP>
 static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t stream) {
