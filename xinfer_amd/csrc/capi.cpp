@@ -21,7 +21,7 @@ namespace xattn {
 namespace {
 
 constexpr int kDecodeMaxQueryVectors = 8;  // G * count at or below this: decode kernel
-constexpr int64_t kDecodeTwoRoundItems = 1536;  // one-round decode items from which items take two rounds
+constexpr int64_t kDecodeManyItems = 1536;  // one-round decode items from which items take several rounds
 constexpr int kPrefillTileQ = 128;         // query vectors per prefill work item
 constexpr int64_t kPrefillMinSplitKeys = 512;
 
@@ -215,16 +215,17 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
       if (qv > 0 && qv <= kDecodeMaxQueryVectors) max_qv = std::max(max_qv, qv);
     }
     grp.dec_qr = pow2_at_least(max_qv);
-    // Two rounds per decode item when one-round items would give at least
-    // kDecodeTwoRoundItems blocks: fewer, longer items halve the split
-    // records; small batches keep one round for the parallelism.
+    // kDecodeItemRounds rounds per decode item when one-round items would
+    // give at least kDecodeManyItems blocks: fewer, longer items cut the split
+    // records and per-item work; small batches keep one round for the
+    // parallelism.
     int64_t one_round_items = 0;
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t qv = (int64_t)counts[row0 + r] * G;
       if (qv > 0 && qv <= kDecodeMaxQueryVectors)
         one_round_items += g.Hkv * ceil_div(lengths[row0 + r], decode_tokens_per_item(dp, grp.dec_qr));
     }
-    grp.dec_rounds = one_round_items >= kDecodeTwoRoundItems ? 2 : 1;
+    grp.dec_rounds = one_round_items >= kDecodeManyItems ? kDecodeItemRounds : 1;
     const int tpi = grp.dec_rounds * decode_tokens_per_item(dp, grp.dec_qr);
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t b = row0 + r;

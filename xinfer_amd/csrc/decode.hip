@@ -39,6 +39,7 @@
 // count == 0 is scheduled only for that.
 #include "device_common.h"
 #include "kernel_args.h"
+#include "launch.h"
 
 namespace xattn {
 
@@ -64,10 +65,14 @@ struct DecodeShape {
 
 // An item takes ROUNDS rounds: the block loads and computes TOK_ROUND keys at
 // a time, reusing the registers, and writes one output or record per item.
-// The planner takes two rounds for launches that have many items (measured on
-// MI355X: 2 us faster on a 122 MB D = 256 batch, neutral on the 126 MB D = 128
-// one, and slower on small batches, which then have too few blocks).
-constexpr int kDecodeMaxRounds = 2;
+// The planner takes four rounds for launches that have many items and one
+// otherwise.  Measured on MI355X (decode + merge kernels): a 122 MB D = 256
+// batch 35.3 us with one round, 32.8 with two, 34.1 with three, 31.2 with
+// four, 31.7 with eight; a 126 MB D = 128 batch 27.7, 27.9, 28.4, 27.3 and
+// 34.9 (with eight, fewer blocks than CUs); batches of 45-98 MB were neutral
+// to 0.6 us slower with two rounds, and small batches slower, with too few
+// blocks.
+constexpr int kDecodeRounds = kDecodeItemRounds;
 
 struct DecodeItem {
   int b, h, split, nsplit, cnt, L, t0, t1;
@@ -482,8 +487,8 @@ static hipError_t launch_decode_r(const AttnArgs &a, int qr, int blocks, hipStre
 
 template <int DP>
 static hipError_t launch_decode_d(const AttnArgs &a, int qr, int rounds, int blocks, hipStream_t stream) {
-  static_assert(kDecodeMaxRounds == 2, "rounds dispatch");
-  return rounds == 2 ? launch_decode_r<DP, 2>(a, qr, blocks, stream) : launch_decode_r<DP, 1>(a, qr, blocks, stream);
+  return rounds == kDecodeRounds ? launch_decode_r<DP, kDecodeRounds>(a, qr, blocks, stream)
+                                 : launch_decode_r<DP, 1>(a, qr, blocks, stream);
 }
 
 hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int blocks, hipStream_t stream) {

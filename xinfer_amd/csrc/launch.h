@@ -13,8 +13,9 @@ hipError_t launch_norm_rope(const NormRopeArgs &a, hipStream_t stream);
 hipError_t launch_gemv(const GemvArgs &a, bool fp32, bool vec, hipStream_t stream);
 
 // Keys of one decode round for padded head dim `dp` and `qr` query vectors per
-// KV head (a power of two <= 8); an item of `rounds` rounds (1 or 2) takes
-// rounds times as many.
+// KV head (a power of two <= 8); an item of `rounds` rounds (1 or
+// kDecodeItemRounds) takes rounds times as many.
+constexpr int kDecodeItemRounds = 4;
 int decode_tokens_per_item(int dp, int qr);
 hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int items, hipStream_t stream);
 
