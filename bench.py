@@ -76,17 +76,24 @@ def dominant_kernel(w):
     """Name of the kernel that carries the workload's algorithmic work.
 
     Mirrors the library's kernel choice: head dims pad to 64 / 128 / 256; prefill
-    uses two key halves (8 waves) at 128; decode is instantiated for the
-    power-of-two query vectors per KV head (count * G).
+    uses two waves per query group (8 waves) at 128; decode is instantiated
+    for the power-of-two query vectors per KV head (count * G) and the rounds
+    per item, four when one-round items would number at least 1536 (the
+    planner in capi.cpp), else one.
     """
     dp = 64 if w.dim <= 64 else (128 if w.dim <= 128 else 256)
     if w.kind == "prefill":
         return f"void xattn::prefill_kernel<{dp}, {2 if dp == 128 else 1}>(xattn::AttnArgs)"
-    qv = max(1, max(c for c in w.counts) * (w.heads // w.kv_heads))
+    group = w.heads // w.kv_heads
+    qv = max(1, max(c for c in w.counts) * group)
     qr = 1
     while qr < qv:
         qr *= 2
-    return f"void xattn::decode_kernel<{dp}, {qr}>(xattn::AttnArgs)"
+    keys_per_round = (16384 if qr <= 4 else 8192) // dp
+    one_round_items = sum(w.kv_heads * -(-length // keys_per_round)
+                          for count, length in zip(w.counts, w.lengths) if count > 0)
+    rounds = 4 if one_round_items >= 1536 else 1
+    return f"void xattn::decode_kernel<{dp}, {qr}, {rounds}>(xattn::AttnArgs)"
 
 
 def record_traffic(fetch_csv, write_csv):
