@@ -232,6 +232,126 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     for (int cc = 0; cc < CPL; ++cc) d = dot8_bf16(r.k[nb][u][cc], r.q[j][cc], d);
     return group_sum<LPT>(d);
   };
+  // Two or four query vectors over 16 or 32 lanes per key row: reduce-scatter
+  // the dot products, so each lane takes the score, weight and row sum of one
+  // query (lane & (QR - 1)) instead of all of them, and fetches the other
+  // queries' weights from its quad for the accumulation.
+  constexpr bool RS = (QR == 2 || QR == 4) && (LPT == 16 || LPT == 32) && CPL == 1;
+  if constexpr (RS) {
+    const int jq = lane & (QR - 1);
+    int lim_q = lim[0];
+#pragma unroll
+    for (int j = 1; j < QR; ++j) lim_q = jq == j ? lim[j] : lim_q;
+    float scq[NB][U], lq = 0.0f;
+    auto score_q = [&](int nb, int u) {
+      float d[QR];
+#pragma unroll
+      for (int j = 0; j < QR; ++j) d[j] = dot8_bf16(r.k[nb][u][0], r.q[j][0], 0.0f);
+      return rs_sum<QR, LPT>(d, lane);
+    };
+#pragma unroll
+    for (int round = 0; round < ROUNDS; ++round) {
+      if (round > 0) {
+        if (it.t0 + round * S::TOK_ROUND >= it.t1) break;  // block-uniform: the item ends earlier
+        issue_item(a, it, r, wave, slot, dc, round);
+      }
+      const int wb = it.t0 + round * S::TOK_ROUND + wave * S::TOK_WAVE;
+      const int we = min(it.t1, wb + S::TOK_WAVE);
+      const bool masked = wb + S::TOK_WAVE > we || wb + S::TOK_WAVE - 1 > it.L - it.cnt;
+      if (masked) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const int tok = wb + nb * BLK + u * TPW + slot;
+            const float sv = score_q(nb, u);
+            scq[nb][u] = (tok < we && tok <= lim_q) ? sv : -INFINITY;
+          }
+      } else {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int u = 0; u < U; ++u) scq[nb][u] = score_q(nb, u);
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int u = 0; u < U; ++u) mx = fmaxf(mx, scq[nb][u]);
+      const float mt_q = slot_max<LPT>(mx) * c;
+      float alpha_q = 1.0f;
+#pragma unroll
+      for (int j = 0; j < QR; ++j) {
+        float mt;
+        if constexpr (QR == 4) {
+          mt = j == 0 ? quad_query<4, 0>(mt_q) : j == 1 ? quad_query<4, 1>(mt_q)
+                                                         : j == 2 ? quad_query<4, 2>(mt_q) : quad_query<4, 3>(mt_q);
+        } else {
+          mt = j == 0 ? quad_query<2, 0>(mt_q) : quad_query<2, 1>(mt_q);
+        }
+        if (round == 0) {
+          m[j] = mt;
+#pragma unroll
+          for (int e = 0; e < F; ++e) acc[j][e] = 0.0f;
+        } else {
+          const float m_new = fmaxf(m[j], mt);
+          const float alpha = fast_exp2(m[j] - (m_new == -INFINITY ? 0.0f : m_new));  // m = -inf: 0
+          alpha_q = jq == j ? alpha : alpha_q;
+#pragma unroll
+          for (int e = 0; e < F; ++e) acc[j][e] *= alpha;
+          m[j] = m_new;
+        }
+      }
+      lq *= alpha_q;
+      float mq = m[0];
+#pragma unroll
+      for (int j = 1; j < QR; ++j) mq = jq == j ? m[j] : mq;
+      const float mu_q = mq == -INFINITY ? 0.0f : mq;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        float p[QR][U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+          const float pq = fast_exp2(fmaf(scq[nb][u], c, -mu_q));
+          lq += pq;
+          if constexpr (QR == 4) {
+            p[0][u] = quad_query<4, 0>(pq);
+            p[1][u] = quad_query<4, 1>(pq);
+            p[2][u] = quad_query<4, 2>(pq);
+            p[3][u] = quad_query<4, 3>(pq);
+          } else {
+            p[0][u] = quad_query<2, 0>(pq);
+            p[1][u] = quad_query<2, 1>(pq);
+          }
+        }
+#pragma unroll
+        for (int e = 0; e < F; ++e) {
+          float vf[U];
+#pragma unroll
+          for (int u = 0; u < U; ++u) {
+            const uint32_t w = r.v[nb][u][e / 8][(e % 8) >> 1];
+            vf[u] = (e & 1) ? bf16_hi(w) : bf16_lo(w);
+          }
+#pragma unroll
+          for (int j = 0; j < QR; ++j) {
+            float t = acc[j][e];
+#pragma unroll
+            for (int u = 0; u < U; ++u) t = fmaf(p[j][u], vf[u], t);
+            acc[j][e] = t;
+          }
+        }
+      }
+    }
+    if constexpr (QR == 4) {
+      l[0] = quad_query<4, 0>(lq);
+      l[1] = quad_query<4, 1>(lq);
+      l[2] = quad_query<4, 2>(lq);
+      l[3] = quad_query<4, 3>(lq);
+    } else {
+      l[0] = quad_query<2, 0>(lq);
+      l[1] = quad_query<2, 1>(lq);
+    }
+  } else
 #pragma unroll
   for (int round = 0; round < ROUNDS; ++round) {
     if (round > 0) {

@@ -67,19 +67,6 @@ constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141; // lane i <-> 7-i within each 8-lane half row
 constexpr int kDppMirror = 0x140;     // lane i <-> 15-i within each 16-lane row
 
-// All-reduce (sum) over aligned groups of N lanes, N in {8,16,32,64}.  Every lane
-// of a group ends with the same value (each level adds a pair of equal partials).
-template <int N>
-__device__ __forceinline__ float group_sum(float x) {
-  x += dpp_move<kDppXor1>(x);
-  x += dpp_move<kDppXor2>(x);
-  x += dpp_move<kDppHalfMirror>(x);
-  if constexpr (N >= 16) x += dpp_move<kDppMirror>(x);
-  if constexpr (N >= 32) x += __shfl_xor(x, 16);
-  if constexpr (N >= 64) x += __shfl_xor(x, 32);
-  return x;
-}
-
 // All-reduce over lanes {l, l ^ 16} / {l, l ^ 32} with the gfx950 permlane
 // swaps.  A swap of x with itself returns x's even-row (lower-half) and
 // odd-row (upper-half) copies in its two results; their sum / max is the
@@ -101,6 +88,21 @@ __device__ __forceinline__ float pair_max32(float x) {
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 constexpr int kDppRowRor8 = 0x128;    // lane i <- lane (i + 8) mod 16 within each row
+constexpr int kDppRowRor4 = 0x124;    // lane i <- lane (i + 4) mod 16 within each row
+
+// All-reduce (sum) over aligned groups of N lanes, N in {8,16,32,64}.  Every lane
+// of a group ends with the same value (each level adds a pair of equal partials).
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  x += dpp_move<kDppXor1>(x);
+  x += dpp_move<kDppXor2>(x);
+  x += dpp_move<kDppHalfMirror>(x);
+  if constexpr (N >= 16) x += dpp_move<kDppMirror>(x);
+  if constexpr (N >= 32) x = pair_sum16(x);
+  if constexpr (N >= 64) x += __shfl_xor(x, 32);
+  return x;
+}
+
 
 // Reductions over the lanes l, l + S, l + 2S, ... (S = stride, a power of two
 // >= 8): the key-row slots of a wave in the decode kernel.
@@ -117,6 +119,41 @@ __device__ __forceinline__ float slot_max(float x) {
   if constexpr (S <= 16) x = pair_max16(x);
   if constexpr (S <= 32) x = pair_max32(x);
   return x;
+}
+
+// Reduce-scatter of QR (2 or 4) per-lane partial dot products over aligned
+// groups of N (16 or 32) lanes: lane l ends with the group's full sum for
+// query l & (QR - 1).  The first log2(QR) steps halve the values each lane
+// keeps (DPP xor 1, xor 2); the rest all-reduce over the lanes of one query
+// with symmetric steps (xor 2 for QR = 2, rotate 8 then rotate 4 within the
+// 16-lane row, the permlane16 pair), so those lanes end with equal sums.
+template <int QR, int N>
+__device__ __forceinline__ float rs_sum(const float (&d)[QR], int lane) {
+  static_assert((QR == 2 || QR == 4) && (N == 16 || N == 32), "reduce-scatter shape");
+  const bool b0 = lane & 1;
+  float v;
+  if constexpr (QR == 4) {
+    const float k0 = b0 ? d[1] : d[0], k1 = b0 ? d[3] : d[2];
+    const float s0 = b0 ? d[0] : d[1], s1 = b0 ? d[2] : d[3];
+    const float n0 = k0 + dpp_move<kDppXor1>(s0), n1 = k1 + dpp_move<kDppXor1>(s1);
+    const bool b1 = lane & 2;
+    const float kk = b1 ? n1 : n0, ss = b1 ? n0 : n1;
+    v = kk + dpp_move<kDppXor2>(ss);
+  } else {
+    const float k0 = b0 ? d[1] : d[0], s0 = b0 ? d[0] : d[1];
+    v = k0 + dpp_move<kDppXor1>(s0);
+    v += dpp_move<kDppXor2>(v);
+  }
+  v += dpp_move<kDppRowRor8>(v);
+  v += dpp_move<kDppRowRor4>(v);
+  if constexpr (N == 32) v = pair_sum16(v);
+  return v;
+}
+// Value of query J from the lane of the quad that holds it (after rs_sum).
+template <int QR, int J>
+__device__ __forceinline__ float quad_query(float x) {
+  constexpr int ctrl = QR == 4 ? J * 0x55 : (J == 0 ? 0xA0 : 0xF5);
+  return dpp_move<ctrl>(x);
 }
 
 __device__ __forceinline__ float wave_max(float x) {
