@@ -151,12 +151,12 @@ __device__ __forceinline__ void load_query(const DecodeParams &a, const DecodeIt
 // into the row, zeroed past D).
 template <int DP, int QR>
 __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeItem &it, DecodeRegs<DP, QR> &r,
-                                           int wave, int slot, int dc, int round = 0) {
+                                           int wave, int slot, int dc, int round = 0, int part = 0) {
   using S = DecodeShape<DP, QR>;
   if (it.cnt == 0) return;
   // The query first: its loads complete before the K/V rows the first dot needs.
   if constexpr (QR <= 4) {
-    if (round == 0) load_query(a, it, r, dc);  // wider groups load it in process_item
+    if (round == 0 && part == 0) load_query(a, it, r, dc);  // wider groups load it in process_item
   }
   const uint32_t row_bytes_k = (uint32_t)(a.k.st * 2), row_bytes_v = (uint32_t)(a.v.st * 2);
   const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
@@ -172,6 +172,7 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
     vv[c] = (uint32_t)first * row_bytes_v + chunk * 16;
   }
   // Every K row before any V row: the scores need all of K, the weights none of V.
+  if (part != 2)
 #pragma unroll
   for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
@@ -179,6 +180,7 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
 #pragma unroll
       for (int c = 0; c < S::CPL; ++c)
         r.k[nb][u][c] = buffer_load16_stream(rk, vk[c], (nb * S::BLK + u * S::TPW) * row_bytes_k);
+  if (part != 1)
 #pragma unroll
   for (int nb = 0; nb < S::NB; ++nb)
 #pragma unroll
@@ -251,10 +253,10 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
     };
 #pragma unroll
     for (int round = 0; round < ROUNDS; ++round) {
-      if (round > 0) {
-        if (it.t0 + round * S::TOK_ROUND >= it.t1) break;  // block-uniform: the item ends earlier
-        issue_item(a, it, r, wave, slot, dc, round);
-      }
+      if (round > 0 && it.t0 + round * S::TOK_ROUND >= it.t1) break;  // block-uniform: the item ends earlier
+      // The next round's rows are loaded while this one computes: K once the
+      // scores have read this round's K, V once the accumulation has read V.
+      const bool next = round + 1 < ROUNDS && it.t0 + (round + 1) * S::TOK_ROUND < it.t1;
       const int wb = it.t0 + round * S::TOK_ROUND + wave * S::TOK_WAVE;
       const int we = min(it.t1, wb + S::TOK_WAVE);
       const bool masked = wb + S::TOK_WAVE > we || wb + S::TOK_WAVE - 1 > it.L - it.cnt;
@@ -273,6 +275,7 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
 #pragma unroll
           for (int u = 0; u < U; ++u) scq[nb][u] = score_q(nb, u);
       }
+      if (next) issue_item(a, it, r, wave, slot, dc, round + 1, 1);
       float mx = -INFINITY;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
@@ -341,6 +344,7 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
           }
         }
       }
+      if (next) issue_item(a, it, r, wave, slot, dc, round + 1, 2);
     }
     if constexpr (QR == 4) {
       l[0] = quad_query<4, 0>(lq);
