@@ -135,9 +135,10 @@ struct PrefillShape {
   static constexpr int NDS = DP / 16;                 // k-steps of the QK product
   static constexpr int NDT = DP / 32;                 // 32-row d tiles of the output
   static constexpr int CHUNKS = DP / 8;               // 16-byte chunks per key row
-  // D = 256 keeps the query tile in LDS for the whole item and reads its Qᵀ
-  // operands from there (held in registers they would leave no room for the
-  // 128 accumulator registers), over 32-key tiles.
+  // D = 256 (one wave per SIMD, 128 accumulator registers, 32-key tiles)
+  // stages the query tile in its own LDS region and keeps each wave's 64 Qᵀ
+  // operand registers in AGPRs, which MFMA reads as its B operand directly
+  // (the VGPRs hold the accumulators).
   static constexpr bool QLDS = DP == 256;
   static constexpr int BN = QLDS ? 32 : kBN;          // keys per tile
   static constexpr int TILE = BN * DP;                // bf16 elements of one K (or V) tile
@@ -326,21 +327,17 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     if (!(wave_active && kw <= wave_kmax && kw < ks1)) return;
     f32x16 s[NKT];
     if constexpr (S::QLDS) {
-      // Qᵀ operands come from the resident query tile: this wave's rows are
-      // stored with the same swizzle as the K rows of its lanes, so both take
-      // the offsets k_off.  Operands are read in groups of two k-steps, one
-      // group ahead of the MFMAs, and the scheduler may not hoist further:
-      // the 128 accumulator registers leave no room for more.
-      static_assert(KH == 1 && NKT == 1, "query tile in LDS: one key slice of 32-key tiles");
-      const uint16_t *Qw = qtile + qgroup * 32 * DP;
+      // Qᵀ operands from AGPRs (read at tile 0); K operands from LDS in groups
+      // of two k-steps, one group ahead of the MFMAs, and the scheduler may
+      // not hoist further: the 128 accumulator registers leave no room for
+      // more.  Measured on cfg5: 546.8 -> 539.2 us against Qᵀ read from LDS
+      // next to each K operand (a third of the tile's LDS reads).
+      static_assert(KH == 1 && NKT == 1, "D = 256 layout: one key slice of 32-key tiles");
       constexpr int GR = 2;
-      u32x4 ka[2][GR], qa[2][GR];
+      u32x4 ka[2][GR];
       auto load = [&](int g, int buf) {
 #pragma unroll
-        for (int u = 0; u < GR; ++u) {
-          ka[buf][u] = *reinterpret_cast<const u32x4 *>(Kt + k_off[g * GR + u]);
-          qa[buf][u] = *reinterpret_cast<const u32x4 *>(Qw + k_off[g * GR + u]);
-        }
+        for (int u = 0; u < GR; ++u) ka[buf][u] = *reinterpret_cast<const u32x4 *>(Kt + k_off[g * GR + u]);
       };
 #pragma unroll
       for (int r = 0; r < 16; ++r) s[0][r] = 0.0f;
@@ -349,7 +346,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       for (int g = 0; g < NDS / GR; ++g) {
         if (g + 1 < NDS / GR) load(g + 1, (g + 1) & 1);
 #pragma unroll
-        for (int u = 0; u < GR; ++u) s[0] = mfma32(as_bf16x8(ka[g & 1][u]), as_bf16x8(qa[g & 1][u]), s[0]);
+        for (int u = 0; u < GR; ++u) s[0] = mfma32(as_bf16x8(ka[g & 1][u]), qf[g * GR + u], s[0]);
         __builtin_amdgcn_sched_barrier(0);
       }
     } else {
@@ -459,11 +456,15 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // a second barrier frees its buffer (the last stage).
   constexpr int PER_TILE = 2 * LOADS;  // load instructions per tile per thread
   auto read_query = [&]() {
-    if constexpr (!S::QLDS) {
 #pragma unroll
-      for (int ds = 0; ds < NDS; ++ds)
-        qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qtile + jr0 * DP +
-                                                             (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+    for (int ds = 0; ds < NDS; ++ds)
+      qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qtile + jr0 * DP +
+                                                           (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
+    if constexpr (S::QLDS) {
+      // One wave per SIMD leaves the AGPRs free: the Qᵀ operands live there
+      // for the item (MFMA reads its B operand from AGPRs directly).
+#pragma unroll
+      for (int ds = 0; ds < NDS; ++ds) asm volatile("" : "+a"(qf[ds]));
     }
     wait_lds_and_barrier();
   };
