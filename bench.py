@@ -613,6 +613,39 @@ def measure_graph_decode(steps, warmup):
 
 
 COPY_PROBE_BYTES = 256 << 20
+STREAM_COPY_BYTES = 1 << 30
+
+
+def stream_copy_bandwidth():
+    """Measured HBM bandwidth of a plain device copy, the secondary denominator of the decode rooflines.
+
+    An elementwise copy (dst = -src) of STREAM_COPY_BYTES, four times the
+    Infinity Cache, so both the read and the write go to HBM; the rate counts
+    the bytes read plus the bytes written, as the decode rooflines count the
+    K/V bytes read.  HIP events on the current stream, median of 9 launches
+    after 2 untimed ones.
+    """
+    import torch
+
+    src = torch.ones(STREAM_COPY_BYTES // 4, dtype=torch.int32, device="cuda")
+    dst = torch.empty_like(src)
+    stream = torch.cuda.current_stream()
+    times = []
+    for i in range(11):
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        torch.neg(src, out=dst)
+        end.record(stream)
+        end.synchronize()
+        if i >= 2:
+            times.append(start.elapsed_time(end) / 1e3)
+    del src, dst
+    torch.cuda.empty_cache()
+    seconds = sorted(times)[len(times) // 2]
+    gbs = 2 * STREAM_COPY_BYTES / seconds / 1e9
+    log(f"[bench] stream copy: 2 x {STREAM_COPY_BYTES} B in {seconds * 1e6:.1f} us = {gbs:.1f} GB/s")
+    return {"GBs": round(gbs, 1), "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4),
+            "kernel": "elementwise int32 copy (torch.neg), read + write counted", "bytes_per_launch": 2 * STREAM_COPY_BYTES}
 
 
 def copy_probe():
@@ -704,6 +737,7 @@ def main():
                                           "frac": round(r["roofline"]["frac"], 4),
                                           "ms_per_step": r["ms_per_step"]} for r in picked}), flush=True)
         return
+    stream_copy = stream_copy_bandwidth()
     prefill = measure(2, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     decode = measure(3, 0, args.steps, args.warmup, not args.eager, with_cpu, args.cpu_budget)
     extra = []
@@ -734,6 +768,11 @@ def main():
         "cpu_baseline": prefill.get("cpu_baseline"),
         "decode": decode,
     }
+    # Secondary denominator of the bandwidth-bound rooflines: the measured copy rate.
+    line["stream_copy"] = stream_copy
+    for r in [decode] + extra:
+        if r["roofline"]["bound"] == "hbm":
+            r["roofline"]["frac_of_stream_copy"] = round(r["roofline"]["achieved"] / stream_copy["GBs"], 4)
     if extra:
         line["configs"] = extra
         seeds = [decode] + [r for r in extra if r["workload"].startswith("cfg3_")]
@@ -743,7 +782,8 @@ def main():
         # bytes over the total attention-op time of the eight batches.
         line["decode_seeds_0_7"] = {"kv_bytes": moved, "attention_op_us": round(op_us, 2),
                                     "GBs": round(moved / op_us / 1e3, 1),
-                                    "frac_hbm": round(moved / op_us / 1e3 / HBM_PEAK_GBS, 4)}
+                                    "frac_hbm": round(moved / op_us / 1e3 / HBM_PEAK_GBS, 4),
+                                    "frac_of_stream_copy": round(moved / op_us / 1e3 / stream_copy["GBs"], 4)}
         log(f"[bench] cfg3 seeds 0-7 aggregate: {moved} B in {op_us:.1f} us = {moved / op_us / 1e3:.1f} GB/s")
         line["summary"] = {r["workload"]: {"attention_op_us": round(r["attention_op_us"], 2),
                                            "achieved": round(r["roofline"]["achieved"], 1),
