@@ -465,10 +465,13 @@ def measure_norm_rope(index, seed, iters=200):
     against the reference adapter's eager modules (transformers Qwen3RMSNorm,
     apply_rotary_pos_emb, then the append), on one workload's token shape.
 
-    Both are timed as eager launch loops with HIP events on the current stream
-    (the eager sequence is about ten kernels; the fused step is one).  Bytes
-    are algorithmic: the projections, cos/sin and weights read once, the query
-    and the appended key/value rows written once.
+    Both are timed as graph replays of at least 50 calls with HIP events on the
+    current stream (the eager sequence is about ten kernels; the fused step is
+    one).  The calls rotate through copies of the projections and cos/sin
+    (enough that their reads exceed twice the Infinity Cache between two uses
+    of a copy, at most 64), so large token shapes read their inputs from HBM.
+    Bytes are algorithmic: the projections, cos/sin and weights read once, the
+    query and the appended key/value rows written once.
     """
     import torch
     from transformers.models.qwen3.modeling_qwen3 import Qwen3RMSNorm, apply_rotary_pos_emb
@@ -478,12 +481,21 @@ def measure_norm_rope(index, seed, iters=200):
     w = workloads.config(index, seed)
     batch, tokens, heads, kv_heads, dim = w.batch, w.tokens, w.heads, w.kv_heads, w.dim
     g = torch.Generator().manual_seed(seed)
-    q = torch.randn(batch, tokens, heads, dim, generator=g).to(torch.bfloat16).cuda()
-    k = torch.randn(batch, tokens, kv_heads, dim, generator=g).to(torch.bfloat16).cuda()
-    v = torch.randn_like(k)
+    q0 = torch.randn(batch, tokens, heads, dim, generator=g).to(torch.bfloat16).cuda()
+    k0 = torch.randn(batch, tokens, kv_heads, dim, generator=g).to(torch.bfloat16).cuda()
+    v0 = torch.randn_like(k0)
     weights = [torch.ones(dim, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
     angle = torch.rand(batch, tokens, dim, generator=g).cuda()
-    cos, sin = angle.cos().to(torch.bfloat16), angle.sin().to(torch.bfloat16)
+    cos0, sin0 = angle.cos().to(torch.bfloat16), angle.sin().to(torch.bfloat16)
+    read_per_call = (q0.numel() + 2 * k0.numel() + 2 * cos0.numel()) * 2
+    copies = min(64, max(2, -(-2 * MALL_BYTES // read_per_call) + 1))
+    inputs = [(q0, k0, v0, cos0, sin0)] + [tuple(x.clone() for x in (q0, k0, v0, cos0, sin0))
+                                            for _ in range(copies - 1)]
+    turn = [0]
+
+    def next_inputs():
+        turn[0] += 1
+        return inputs[turn[0] % copies]
     positions = torch.stack([torch.arange(p, p + tokens) for p in w.prefixes]).cuda()
     cu = torch.tensor([0] + torch.tensor(w.counts).cumsum(0).tolist(), dtype=torch.int32, device="cuda")
     cache = [torch.zeros(batch, kv_heads, w.capacity, dim, dtype=torch.bfloat16, device="cuda") for _ in range(2)]
@@ -495,26 +507,47 @@ def measure_norm_rope(index, seed, iters=200):
         norms.append(norm)
 
     def fused():
+        q, k, v, cos, sin = next_inputs()
         qk_norm_rope_append(q, k, v, weights[0], weights[1], 1e-6, cos, sin, positions, cu, cache[0], cache[1])
 
     def eager():
+        q, k, v, cos, sin = next_inputs()
         qh = norms[0](q).transpose(1, 2)
         kh = norms[1](k).transpose(1, 2)
         qh, kh = apply_rotary_pos_emb(qh, kh, cos, sin)
         torch.ops.xinfer.append_kv_batched(kh, v.transpose(1, 2), positions, cu, cache[0], cache[1])
 
-    def per_call_us(function):
+    def per_call_us(function, per_graph=max(50, copies), replays=20):
+        # Device time per call: HIP events around replays of a graph of
+        # `per_graph` calls (the serving loop's launch path); eager launches if
+        # capture fails.
         with torch.inference_mode():
             for _ in range(20):
                 function()
-            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
-            start.record()
-            for _ in range(iters):
-                function()
-            end.record()
-            end.synchronize()
-        return start.elapsed_time(end) * 1e3 / iters
+            start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            try:
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    for _ in range(per_graph):
+                        function()
+                graph.replay()
+                torch.cuda.synchronize()
+                start.record()
+                for _ in range(replays):
+                    graph.replay()
+                end.record()
+                end.synchronize()
+                return start.elapsed_time(end) * 1e3 / (replays * per_graph)
+            except Exception as error:  # capture unsupported: eager launches
+                log(f"graph capture unavailable ({error}); timing eager launches")
+                torch.cuda.synchronize()
+                start.record()
+                for _ in range(iters):
+                    function()
+                end.record()
+                end.synchronize()
+                return start.elapsed_time(end) * 1e3 / iters
 
     fused_us, eager_us = per_call_us(fused), per_call_us(eager)
     real = sum(w.counts)

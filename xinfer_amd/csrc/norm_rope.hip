@@ -83,10 +83,21 @@ __global__ void __launch_bounds__(256) norm_rope_kernel(const NormRopeArgs a) {
       xn[2 * e] = round_bf16(bf16_lo(w[e]) * round_bf16(xf[2 * e] * inv));
       xn[2 * e + 1] = round_bf16(bf16_hi(w[e]) * round_bf16(xf[2 * e + 1] * inv));
     }
-    // The other half of the row, from the partner lane.
+    // The other half of the row, from the partner lane c ^ LPR/2: DPP
+    // row_ror:8 within a 16-lane row (LPR = 16), the permlane16 swap (LPR =
+    // 32); a shuffle through LDS for LPR = 8.
     float pn[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) pn[e] = __shfl_xor(xn[e], LPR / 2, LPR);
+    for (int e = 0; e < 8; ++e) {
+      if constexpr (LPR == 16) {
+        pn[e] = dpp_move<kDppRowRor8>(xn[e]);
+      } else if constexpr (LPR == 32) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(xn[e]), __float_as_uint(xn[e]), false, false);
+        pn[e] = __uint_as_float(dc < 16 ? r[1] : r[0]);
+      } else {
+        pn[e] = __shfl_xor(xn[e], LPR / 2, LPR);
+      }
+    }
     const bool lower = dc < LPR / 2;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
