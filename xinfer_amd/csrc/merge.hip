@@ -74,11 +74,12 @@ __device__ __forceinline__ void fold_and_write(MergeRed<FS, SG> &red, const floa
       u32x2 ml[INFLIGHT];
       f32x4 o[INFLIGHT];
 #pragma unroll
-      for (int u = 0; u < INFLIGHT; ++u) {
-        const int64_t sp = min(s0 + u * SG, nsplit - 1);
-        ml[u] = *as_global(reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step)));
-        o[u] = *as_global(reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step));
-      }
+      for (int u = 0; u < INFLIGHT; ++u)
+        if (s0 + u * SG < nsplit) {  // a lane loads only its own splits' records
+          const int64_t sp = s0 + u * SG;
+          ml[u] = *as_global(reinterpret_cast<const u32x2 *>(part_ml + 2 * (ml_base + sp * ml_step)));
+          o[u] = *as_global(reinterpret_cast<const f32x4 *>(part_o + o_base + sp * o_step));
+        }
 #pragma unroll
       for (int u = 0; u < INFLIGHT; ++u)
         if (s0 + u * SG < nsplit) fold(st, __uint_as_float(ml[u].x), __uint_as_float(ml[u].y), o[u]);
