@@ -8,7 +8,9 @@ positions, the new tokens and the queries in place (the serving loop's
 per-step writes), runs other eager work and synchronises; every replay must
 equal, bit for bit, the same two operators launched eagerly on a copy of the
 caches, and stay within the oracle gates.  The default operator, whose plan
-comes from host lengths, agrees within the same gates.
+comes from host lengths, agrees within the same gates.  The two decode shapes
+at capacity 16384 take four-round items (one block each), the two-token shape
+one-round items taken in turn by the blocks of a capped grid.
 """
 
 import numpy as np

@@ -225,13 +225,22 @@ def test_graph_mode_shapes_and_workspace(lib):
     """The graph-capture entry point plans from shapes alone: its workspace
     holds every row's records at capacity, and rows that would take the
     prefill kernel (T * Hq/Hkv > 8) or more than 64 rows are refused before
-    any launch."""
+    any launch.  Items take four rounds of 128 keys (D = 128, two query
+    vectors per KV head) when the capacity layout holds at least 1536
+    one-round items and at most 2048 four-round ones, else one round."""
     lib.xinfer_batched_flash_attention_graph_workspace_size.restype = ctypes.c_size_t
-    q, k = view([8, 16, 1, 128]), view([8, 8, 16384, 128])
-    size = lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(q), ctypes.byref(k))
-    splits = 16384 // 128  # keys per decode item at D = 128 with two query vectors per KV head
-    records = 8 * 8 * splits * 2
-    assert size == -(-records * 128 * 4 // 256) * 256 + records * 8
+
+    def workspace(batch, capacity):
+        q, k = view([batch, 16, 1, 128]), view([batch, 8, capacity, 128])
+        return lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(q), ctypes.byref(k))
+
+    def records_bytes(batch, splits):
+        records = batch * 8 * splits * 2
+        return -(-records * 128 * 4 // 256) * 256 + records * 8
+
+    assert workspace(8, 16384) == records_bytes(8, 16384 // 512)   # 8192 one-round items -> four rounds
+    assert workspace(1, 4096) == records_bytes(1, 4096 // 128)     # 256 one-round items
+    assert workspace(16, 16384) == records_bytes(16, 16384 // 128)  # 4096 four-round items: one round
     assert lib.xinfer_status_string(18).decode().startswith("Graph-capture attention takes decode rows")
 
     def graph(qv, kv):

@@ -392,14 +392,18 @@ int check_batched(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
 // one row table (B <= kMaxRows, which the kernels' per-block tables assume).
 // Records are laid out for every row at capacity.
 struct CapturePlan {
-  int dp = 0, qr = 1, tok_item = 0, splits_max = 0, decode_blocks = 0;
+  int dp = 0, qr = 1, rounds = 1, tok_item = 0, splits_max = 0, decode_blocks = 0;
   int64_t row_records = 0, records = 0;
   size_t part_ml_offset() const { return (size_t)((records * dp_d * 4 + 255) / 256 * 256); }
   size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
   int64_t dp_d = 0;  // the head dim D (records hold D floats)
 };
 // Decode blocks of a capture launch: every item of the capacity layout, at
-// most eight per CU of the 256 (the blocks take the valid items in turn).
+// most eight per CU of the 256.  With one-round items the blocks take the
+// valid items in turn; multi-round items (kDecodeItemRounds rounds, chosen
+// when the capacity layout has as many one-round items as the default
+// planner's threshold and its multi-round items fit this grid) take one block
+// each.
 constexpr int kCaptureMaxBlocks = 2048;
 
 int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v, Geometry &g,
@@ -416,7 +420,11 @@ int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
   cp.dp = padded_dim(g.D);
   cp.dp_d = g.D;
   cp.qr = pow2_at_least((int)std::max<int64_t>(1, g.T * G));
-  cp.tok_item = decode_tokens_per_item(cp.dp, cp.qr);
+  const int tok_round = decode_tokens_per_item(cp.dp, cp.qr);
+  const int64_t one_round_items = g.B * g.Hkv * ceil_div(g.C, tok_round);
+  const int64_t multi_round_items = g.B * g.Hkv * ceil_div(g.C, (int64_t)kDecodeItemRounds * tok_round);
+  cp.rounds = one_round_items >= kDecodeManyItems && multi_round_items <= kCaptureMaxBlocks ? kDecodeItemRounds : 1;
+  cp.tok_item = cp.rounds * tok_round;
   cp.splits_max = (int)ceil_div(g.C, cp.tok_item);
   cp.row_records = g.Hkv * cp.splits_max * g.T * G;
   cp.records = cp.splits_max > 1 ? g.B * cp.row_records : 0;
@@ -536,7 +544,7 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
   c.row_records = cp.row_records;
   c.total_items = (int32_t)(g.B * g.Hkv * cp.splits_max);
   const hipStream_t s = static_cast<hipStream_t>(stream);
-  if (launch_decode_capture(c, cp.dp, cp.qr, cp.decode_blocks, s) != hipSuccess) return XINFER_ERR_LAUNCH;
+  if (launch_decode_capture(c, cp.dp, cp.qr, cp.rounds, cp.decode_blocks, s) != hipSuccess) return XINFER_ERR_LAUNCH;
   if (cp.splits_max > 1) {
     c.total_items = (int32_t)(g.B * g.Hkv * g.T * c.G);
     if (launch_merge_capture(c, cp.dp, cp.splits_max, s) != hipSuccess) return XINFER_ERR_LAUNCH;

@@ -522,7 +522,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
 // for a row without queries), and takes items blockIdx.x, blockIdx.x +
 // gridDim.x, ... of that list, so the valid items are spread evenly over the
 // grid whatever the lengths; blocks past the list exit after the one read.
-template <int DP, int QR>
+template <int DP, int QR, int ROUNDS>
 __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c) {
   using S = DecodeShape<DP, QR>;
   __shared__ DecodeShared<DP, QR> sh;
@@ -548,7 +548,11 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
   __syncthreads();
   const int total = row_first[c.B];
   const DecodeParams p{c.q, c.k, c.v, c.out, c.o_sb, c.o_sh, c.o_st, c.part_o, c.part_ml, c.scale_log2, c.D, c.G, c.T};
-  for (int item = blockIdx.x; item < total; item += gridDim.x) {
+  // One-round items: blocks take items blockIdx.x, blockIdx.x + gridDim.x, ...
+  // Multi-round items: the grid covers every item of the capacity layout, one
+  // block each (a loop would keep the next round's loads and the item state
+  // live across iterations and double the registers).
+  for (int item = blockIdx.x; item < total; item += (ROUNDS == 1 ? (int)gridDim.x : total)) {
     int r = 0;
     while (row_first[r + 1] <= item) ++r;
     RowSched rs;
@@ -559,30 +563,35 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
     rs.nsplit = row_splits[r];
     rs.ntiles = 1;
     rs.rec_begin = (int64_t)r * c.row_records;
-    const DecodeItem it = locate_item(rs, item, S::TOK_ROUND);
+    const DecodeItem it = locate_item(rs, item, ROUNDS * S::TOK_ROUND);
     DecodeRegs<DP, QR> regs;
     issue_item(p, it, regs, wave, slot, dc);
-    process_item<DP, QR, 1>(p, it, regs, sh, wave, lane, slot, dc);
+    process_item<DP, QR, ROUNDS>(p, it, regs, sh, wave, lane, slot, dc);
+    if (ROUNDS > 1) break;
     __syncthreads();  // the next item reuses the block's reduction buffers
   }
 }
 
-template <int DP>
-static hipError_t launch_decode_capture_d(const CaptureArgs &c, int qr, int blocks, hipStream_t stream) {
+template <int DP, int ROUNDS>
+static hipError_t launch_decode_capture_r(const CaptureArgs &c, int qr, int blocks, hipStream_t stream) {
   switch (qr) {
-    case 1: hipLaunchKernelGGL((decode_capture_kernel<DP, 1>), dim3(blocks), dim3(256), 0, stream, c); break;
-    case 2: hipLaunchKernelGGL((decode_capture_kernel<DP, 2>), dim3(blocks), dim3(256), 0, stream, c); break;
-    case 4: hipLaunchKernelGGL((decode_capture_kernel<DP, 4>), dim3(blocks), dim3(256), 0, stream, c); break;
-    default: hipLaunchKernelGGL((decode_capture_kernel<DP, 8>), dim3(blocks), dim3(256), 0, stream, c); break;
+    case 1: hipLaunchKernelGGL((decode_capture_kernel<DP, 1, ROUNDS>), dim3(blocks), dim3(256), 0, stream, c); break;
+    case 2: hipLaunchKernelGGL((decode_capture_kernel<DP, 2, ROUNDS>), dim3(blocks), dim3(256), 0, stream, c); break;
+    case 4: hipLaunchKernelGGL((decode_capture_kernel<DP, 4, ROUNDS>), dim3(blocks), dim3(256), 0, stream, c); break;
+    default: hipLaunchKernelGGL((decode_capture_kernel<DP, 8, ROUNDS>), dim3(blocks), dim3(256), 0, stream, c); break;
   }
   return hipGetLastError();
 }
 
-hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int blocks, hipStream_t stream) {
+hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int rounds, int blocks, hipStream_t stream) {
+  const bool multi = rounds == kDecodeRounds;
   switch (dp) {
-    case 64: return launch_decode_capture_d<64>(c, qr, blocks, stream);
-    case 128: return launch_decode_capture_d<128>(c, qr, blocks, stream);
-    default: return launch_decode_capture_d<256>(c, qr, blocks, stream);
+    case 64: return multi ? launch_decode_capture_r<64, kDecodeRounds>(c, qr, blocks, stream)
+                          : launch_decode_capture_r<64, 1>(c, qr, blocks, stream);
+    case 128: return multi ? launch_decode_capture_r<128, kDecodeRounds>(c, qr, blocks, stream)
+                           : launch_decode_capture_r<128, 1>(c, qr, blocks, stream);
+    default: return multi ? launch_decode_capture_r<256, kDecodeRounds>(c, qr, blocks, stream)
+                          : launch_decode_capture_r<256, 1>(c, qr, blocks, stream);
   }
 }
 

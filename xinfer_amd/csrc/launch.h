@@ -27,7 +27,7 @@ hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t 
 // Graph-capture decode: the decode kernel over `blocks` blocks, then the merge
 // of every query vector of the capacity layout; max_splits = splits of a
 // row at capacity picks the merge's thread layout.
-hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int blocks, hipStream_t stream);
+hipError_t launch_decode_capture(const CaptureArgs &c, int dp, int qr, int rounds, int blocks, hipStream_t stream);
 hipError_t launch_merge_capture(const CaptureArgs &c, int dp, int max_splits, hipStream_t stream);
 
 // Bytes of the static device scratch behind the allocation-free entry point
