@@ -520,8 +520,10 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
 // Each block reads every row's count and length once, numbers the row's work
 // items as the default schedule would (Hkv x splits, or Hkv zero-fill items
 // for a row without queries), and takes items blockIdx.x, blockIdx.x +
-// gridDim.x, ... of that list, so the valid items are spread evenly over the
-// grid whatever the lengths; blocks past the list exit after the one read.
+// gridDim.x, ... of that list (ROUNDS > 1: the grid holds every item of the
+// capacity layout, and a block takes item blockIdx.x only), so the valid
+// items are spread evenly over the grid whatever the lengths; blocks past the
+// list exit after the one read.
 template <int DP, int QR, int ROUNDS>
 __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c) {
   using S = DecodeShape<DP, QR>;
