@@ -20,6 +20,8 @@ int decode_tokens_per_item(int dp, int qr);
 hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int items, hipStream_t stream);
 
 hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream);
+// The head-dim-256 prefill kernel over `blocks` blocks (prefill_d256.hip).
+hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t stream);
 
 // Merges a.total_items query vectors; max_splits picks the thread layout.
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream);

@@ -56,6 +56,7 @@
 // The tile-0 / split-0 item zeroes the row's padded queries (t >= count).
 #include "device_common.h"
 #include "kernel_args.h"
+#include "launch.h"
 
 namespace xattn {
 
@@ -608,6 +609,15 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   }
 }
 
+// The D = 256 kernel is built in its own translation unit (prefill_d256.hip
+// includes this file with XATTN_PREFILL_D256 defined), so that it can take
+// its own scheduler flags.
+#ifdef XATTN_PREFILL_D256
+hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t stream) {
+  hipLaunchKernelGGL((prefill_kernel<256, 1>), dim3(blocks), dim3(256), 0, stream, a);
+  return hipGetLastError();
+}
+#else
 // Blocks per launch: 8 times the longest XCD run (blocks past their run exit
 // at once).
 hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream) {
@@ -620,9 +630,10 @@ hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream) {
   switch (dp) {
     case 64: hipLaunchKernelGGL((prefill_kernel<64, 2>), grid, dim3(512), 0, stream, a); break;
     case 128: hipLaunchKernelGGL((prefill_kernel<128, 2>), grid, dim3(512), 0, stream, a); break;
-    default: hipLaunchKernelGGL((prefill_kernel<256, 1>), grid, dim3(256), 0, stream, a); break;
+    default: return launch_prefill_d256(a, grid.x, stream);
   }
   return hipGetLastError();
 }
+#endif
 
 }  // namespace xattn
