@@ -35,13 +35,15 @@ TORCH_SOURCES = ("torch_ops.cpp",)
 # Packed fp32 VALU instructions are kept out of every device build.
 NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 
-# Per-source device flags.  The max-ilp scheduling strategy reorders the
-# decode and head-dim-256 prefill kernels (the same instructions and results)
-# for more overlap; measured on MI355X: cfg5 prefill 541 -> 524 us, cfg4 decode
-# 29.9 -> 29.2 us, cfg3 seed 0 decode 26.1 -> 25.7 us.  The head-dim-64/128
-# prefill kernel keeps the default strategy (cfg2 no faster with it).
+# Per-source scheduling strategies: they reorder the same instructions (the
+# results are bit for bit those of the default scheduler).  Measured on
+# MI355X: max-ilp takes the head-dim-256 prefill from 535 to 516 us (cfg5) and
+# the decode kernels 1-2 % faster; iterative-ilp takes the head-dim-64/128
+# prefill from 21.4 to 20.8 us (cfg2), where max-ilp gained nothing, and made
+# the head-dim-256 kernel 8 % slower.
 SOURCE_FLAGS = {
     "decode.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "prefill_d256.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
 
