@@ -40,9 +40,11 @@ NO_PACKED_FP32 = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
 # MI355X: max-ilp takes the head-dim-256 prefill from 535 to 516 us (cfg5) and
 # the decode kernels 1-2 % faster; iterative-ilp takes the head-dim-64/128
 # prefill from 21.4 to 20.8 us (cfg2), where max-ilp gained nothing, and made
-# the head-dim-256 kernel 8 % slower.
+# the head-dim-256 kernel 8 % slower.  max-ilp also takes the fused
+# norm/RoPE/append kernel from 4.97 to 4.85 us at cfg2's 512 tokens.
 SOURCE_FLAGS = {
     "decode.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
+    "norm_rope.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
     "prefill.hip": ["-mllvm", "-amdgpu-sched-strategy=iterative-ilp"],
     "prefill_d256.hip": ["-mllvm", "-amdgpu-sched-strategy=max-ilp"],
 }
