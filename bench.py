@@ -55,7 +55,9 @@ TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 # one workload each.
 TRAFFIC_WORKLOADS = ("cfg2_prefill_b1_n512_p1536", "cfg3_ragged_decode_b8_seed0", "cfg4_decode_b4_d256",
                      "cfg5_ragged_prefill_b8_seed0")
-KERNEL_SOURCES = ("xinfer_amd/csrc/*.hip", "xinfer_amd/csrc/*.h", "xinfer_amd/csrc/*.cpp")
+# The kernels' sources and the build script, whose per-source compiler flags
+# change the machine code as much as the sources do.
+KERNEL_SOURCES = ("xinfer_amd/csrc/*.hip", "xinfer_amd/csrc/*.h", "xinfer_amd/csrc/*.cpp", "xinfer_amd/build.py")
 
 
 def log(message):
@@ -63,7 +65,7 @@ def log(message):
 
 
 def sources_digest():
-    """Digest of the native sources: a traffic record only applies to the kernels it measured."""
+    """Digest of the native sources and build flags: a traffic record only applies to the kernels it measured."""
     digest = hashlib.sha256()
     for pattern in KERNEL_SOURCES:
         for path in sorted(ROOT.glob(pattern)):
