@@ -415,8 +415,10 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     // key 32kt + 16hh + 8(e/4) + 4half + e%4, i.e. two runs of 4 keys, which the
     // two transposing reads of each A operand supply.
     if constexpr (S::QLDS) {
-      // V operands in groups of two d tiles, one group ahead (as for QK).
-      constexpr int GT = 2;
+      // V operands one d tile ahead of its MFMAs.  Measured on cfg5 (same
+      // outputs): groups of one d tile 504 us, of two 516 us, of four 503 us,
+      // all eight at once 526 us.
+      constexpr int GT = 1;
       u32x4 va[2][GT][2];
       auto load = [&](int g, int buf) {
 #pragma unroll
