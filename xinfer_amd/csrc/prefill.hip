@@ -443,16 +443,30 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       }
       return;
     }
-#pragma unroll
-    for (int t = 0; t < NDT; ++t)
+    // V operands one d tile ahead of their MFMAs (measured on cfg2, same
+    // outputs: 21.2 against 21.5 us with the reads left to the scheduler;
+    // K operands one k-step ahead in the score loop measured slower).
+    u32x4 vop[2][NKT][2];
+    auto vload = [&](int t, int buf) {
 #pragma unroll
       for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
           const uint16_t *vp = Vt + v_off[t] + (kt * 32 + hh * 16) * DP;
           const u32x2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * DP);
-          acc[t] = mfma32(as_bf16x8(u32x4{lo.x, lo.y, hi.x, hi.y}), pb[kt][hh], acc[t]);
+          vop[buf][kt][hh] = u32x4{lo.x, lo.y, hi.x, hi.y};
         }
+    };
+    vload(0, 0);
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) {
+      if (t + 1 < NDT) vload(t + 1, (t + 1) & 1);
+#pragma unroll
+      for (int kt = 0; kt < NKT; ++kt)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) acc[t] = mfma32(as_bf16x8(vop[t & 1][kt][hh]), pb[kt][hh], acc[t]);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   };
 
   // Pipeline.  The query tile is read into registers at tile 0, after which
