@@ -17,9 +17,10 @@ seeds 0-7 together as ``decode_seeds_0_7``, and a per-workload ``summary``.
 
 Timing: each workload keeps several copies of its caches and rotates through
 them so consecutive steps never find their KV in the 256 MB Infinity Cache.
-One step per copy is captured in a HIP graph (the serving loop's launch
-path); the timed region replays exactly K steps between two device
-synchronisations.  The roofline figure of the dominant kernel is measured
+The K timed steps are captured together in one HIP graph (the serving loop's
+launch path), so the timed region is one graph launch of exactly K device
+steps between two device synchronisations, and the host's launch cost is
+paid once rather than per step.  The roofline figure of the dominant kernel is measured
 separately with HIP events on the launch stream around graph replays of the
 attention operator alone, and divides the algorithmic work (KV bytes for
 decode, causal FLOPs for prefill) by that average duration.
@@ -190,7 +191,8 @@ class Runner:
         self.extent = cache_extent(w.lengths[0])
         self.outputs = {}
         self.use_graphs = use_graphs
-        self.step_graphs = self.cycle_graph = self.attention_graph = None
+        self.step_graphs = self.cycle_graph = self.attention_graph = self.timed_graph = None
+        self.timed_count = 0
         self.cycle = self.copies
         self.graph_op = graph_op
 
@@ -207,13 +209,18 @@ class Runner:
         k, v = self.caches[i % self.copies]
         if self.w.append:
             self.torch.ops.xinfer.append_kv_batched(self.new_k, self.new_v, self.positions, self.cu[0], k, v)
-        self.outputs[i] = self.attention(i)
+        # One output per cache copy: a step's output replaces the one of the
+        # step that used the same copy before it.
+        self.outputs[i % self.copies] = self.attention(i)
 
-    def capture(self):
-        """Graphs: one step per cache copy, a cycle of S steps, and S attention-only calls.
+    def capture(self, timed_steps=0):
+        """Graphs: one step per cache copy, a cycle of S steps, S attention-only
+        calls, and the timed graph of exactly ``timed_steps`` steps.
 
         S is a multiple of the copy count covering at least 16 steps, so one replay
-        amortises the host's launch cost over many device steps.
+        amortises the host's launch cost over many device steps.  The timed graph
+        holds the whole timed region, so timing it measures the device steps, not
+        the host's graph launches.
         """
         torch = self.torch
         if not self.use_graphs:
@@ -234,10 +241,18 @@ class Runner:
             with torch.cuda.graph(self.cycle_graph):
                 for i in range(self.cycle):
                     self.step(i)
-            cycle_outputs = [self.outputs[i] for i in range(self.copies)]
+            cycle_outputs = [self.outputs[i % self.copies] for i in range(self.copies)]
             self.attention_graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(self.attention_graph):
                 self.attention_outputs = [self.attention(i) for i in range(self.cycle)]
+            timed_outputs = []
+            if timed_steps > 0:
+                self.timed_graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(self.timed_graph):
+                    for i in range(timed_steps):
+                        self.step(i)
+                timed_outputs = [self.outputs[i % self.copies] for i in range(min(timed_steps, self.copies))]
+                self.timed_count = timed_steps
             # Replays must reproduce the eager results bit for bit.
             for _ in range(2):
                 for graph, _ in self.step_graphs:
@@ -252,14 +267,28 @@ class Runner:
                 for i, (_, out) in enumerate(self.step_graphs):
                     if not (torch.equal(out, eager[i]) and torch.equal(cycle_outputs[i], eager[i])):
                         raise RuntimeError("step graph replay differs from eager execution")
+            if self.timed_graph is not None:
+                # Its first launch also uploads the graph: done here, untimed,
+                # and checked like the others.
+                self.timed_graph.replay()
+                torch.cuda.synchronize()
+                for i, out in enumerate(timed_outputs):
+                    if not torch.equal(out, eager[i]):
+                        raise RuntimeError("timed graph replay differs from eager execution")
             return True
         except Exception as error:  # capture unsupported: fall back to eager launches
             log(f"graph capture unavailable ({error}); timing eager launches")
-            self.step_graphs = self.cycle_graph = self.attention_graph = None
+            self.step_graphs = self.cycle_graph = self.attention_graph = self.timed_graph = None
             self.use_graphs = False
             return False
 
     def run_steps(self, count):
+        """Run `count` steps: one launch of the timed graph when it holds exactly
+        that many, else cycle replays plus single-step replays (warm-up), else
+        eager launches."""
+        if self.timed_graph is not None and count == self.timed_count:
+            self.timed_graph.replay()
+            return
         if self.step_graphs is None:
             for i in range(count):
                 self.step(i)
@@ -404,7 +433,7 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
     inputs = workloads.make_inputs(w)
     runner = Runner(w, inputs, use_graphs)
     with torch.inference_mode():
-        graphs = runner.capture()
+        graphs = runner.capture(steps)
         runner.run_steps(warmup)
         seconds = runner.timed_steps(steps)
         op_seconds = runner.attention_duration(max(steps, 4 * runner.copies))
@@ -421,6 +450,7 @@ def measure(index, seed, steps, warmup, use_graphs, with_cpu, cpu_budget):
         "ms_per_step": seconds * 1e3,
         "attention_op_us": op_seconds * 1e6,
         "graph_replay": graphs,
+        "timed_graph_steps": runner.timed_count,
         "cache_copies": runner.copies,
         "roofline": {
             "bound": "hbm" if decode else "mfma",

@@ -24,8 +24,9 @@ from xinfer_amd.attention import batched_attention_metadata
 pytestmark = pytest.mark.gpu
 
 # (name, Hq, Hkv, D, counts, lengths, capacity).  One-round items per KV head
-# and row are ceil(L / keys per round): 128 keys for padded dim 128 with up
-# to four query vectors, 32 for padded dim 256 with eight.
+# and row are ceil(L / keys per round): 256 keys for padded dim 64 and 128 for
+# padded dim 128 with up to four query vectors, 32 for padded dim 256 with
+# eight.
 CASES = (
     # 8 KV heads x (125 + 94 + 71) = 2320 one-round items; rows of two queries.
     ("two_queries_d128", 16, 8, 128, [2, 1, 2, 0], [16000, 12000, 9000, 5], 16384),
@@ -36,6 +37,14 @@ CASES = (
     # vectors per KV head, the widest decode group (32 keys per round);
     # 4 x (500 + 250 + 65) = 3260 one-round items.
     ("group4_dim200", 16, 4, 200, [2, 1, 1], [16000, 7999, 2049], 16384),
+    # Head dim 64: 256 keys per round, no reduce-scatter of the scores;
+    # 8 x (25 + 28 + 26 + 36 + 24 + 26 + 27) = 1536 one-round items (the
+    # threshold itself), a two-query row, an empty row, partial last rounds.
+    ("dim64", 16, 8, 64, [1, 2, 1, 1, 0, 1, 1, 1], [6200, 7000, 6500, 9000, 3, 6144, 6401, 6657], 9216),
+    # Head dim 40 (padded to 64), one query vector per KV head (G = 1):
+    # 8 x (25 + 26 + 26 + 27 + 24 + 25 + 25 + 26) = 1632 one-round items;
+    # the row of 6145 keys ends one key into its last round.
+    ("odd_dim_40_g1", 8, 8, 40, [1] * 8, [6400, 6600, 6500, 6700, 6144, 6145, 6300, 6500], 8192),
 )
 
 

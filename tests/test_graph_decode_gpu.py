@@ -8,9 +8,16 @@ positions, the new tokens and the queries in place (the serving loop's
 per-step writes), runs other eager work and synchronises; every replay must
 equal, bit for bit, the same two operators launched eagerly on a copy of the
 caches, and stay within the oracle gates.  The default operator, whose plan
-comes from host lengths, agrees within the same gates.  The two decode shapes
-at capacity 16384 take four-round items (one block each), the two-token shape
-one-round items taken in turn by the blocks of a capped grid.
+comes from host lengths, agrees within the same gates.
+
+Launch shapes covered (capi.cpp, check_capture): the Qwen3 and Qwen3.5
+decode shapes and the head-dim-64 shape take four-round items, one block
+each; the two-token shapes take one-round items with one block per item; the
+64-row batch at capacity 16384 has 65536 one-round items in a grid capped at
+2048 blocks, so every block takes several items in turn (blockIdx.x,
+blockIdx.x + 2048, ...) and reuses its reduction buffers between them.  Query
+vectors per KV head: 2 (Qwen3), 4 (Qwen3.5, two tokens), 1 (head dim 64,
+G = 1) and 8 (two tokens with G = 4).
 """
 
 import numpy as np
@@ -40,6 +47,22 @@ SHAPES = {
         [(2, 300), (1, 4096), (0, 5), (2, 2)],
         [(1, 1), (2, 3000), (2, 129), (1, 700)],
     ]),
+    # G = 4 and two tokens: eight query vectors per KV head.
+    "two_tokens_group4": (16, 4, 128, 2, 4096, [
+        [(2, 4096), (1, 77), (2, 1500), (0, 3)],
+        [(2, 2), (2, 4000), (1, 1), (2, 640)],
+    ]),
+    # Head dim 64, G = 1: 256 keys per round, four-round items.
+    "d64_group1": (8, 8, 64, 1, 8192, [
+        [(1, 8192), (1, 5000), (1, 1), (1, 257), (0, 9), (1, 1024), (1, 3333), (1, 7777)],
+        [(1, 3), (1, 8191), (1, 600), (1, 6000), (1, 2), (1, 4097), (0, 1), (1, 1025)],
+    ]),
+    # 64 rows at capacity 16384: a grid capped at 2048 blocks over up to
+    # 65536 items, with ragged and empty rows.
+    "capped_grid_b64": (16, 8, 128, 1, 16384, [
+        [(0 if r % 13 == 5 else 1, (r * 2654435761) % 16384 + 1) for r in range(64)],
+        [(0 if r % 7 == 3 else 1, 16384 if r % 9 == 0 else (r * 40503) % 3000 + 1) for r in range(64)],
+    ]),
 }
 
 
@@ -50,15 +73,16 @@ def metadata(rows):
 
 
 def check_oracle(out, q, k, v, rows, scale):
-    counts, lengths = [c for c, _ in rows], [n for _, n in rows]
-    expected = oracle.attention(*(x.float().cpu().numpy().astype(np.float64) for x in (q, k, v)), counts, lengths,
-                                scale)
+    """Each row against the float64 oracle over its own populated prefix only."""
     out = out.cpu()
-    for r, count in enumerate(counts):
+    for r, (count, length) in enumerate(rows):
         assert torch.count_nonzero(out[r, :, count:]).item() == 0
         if count:
+            expected = oracle.attention(*(x[r : r + 1, :, :n].float().cpu().numpy().astype(np.float64)
+                                          for x, n in ((q, count), (k, length), (v, length))),
+                                        [count], [length], scale)
             errors = row_errors(out[r, :, :count].float().flatten(1),
-                                torch.from_numpy(expected[r, :, :count]).float().flatten(1))
+                                torch.from_numpy(expected[0]).float().flatten(1))
             assert errors["max_abs"] <= MAX_ABS and errors["mean_abs"] <= MEAN_ABS, (r, errors)
 
 

@@ -7,10 +7,17 @@ a 512-token prefill chunk whose records fill half of the scratch, then a
 smaller ragged decode batch -- must each equal the workspace entry point bit
 for bit (the second call finds the first call's records in the scratch and
 must not depend on them), and stay within the oracle gates.  A plan beyond
-the scratch is refused before any launch.
+the scratch is refused before any launch.  In a fresh process, the first
+call (which looks up the scratch's device address) is made while a HIP graph
+is being captured; every replay of that graph must equal the workspace entry
+point bit for bit.
 """
 
 import ctypes
+import os
+import subprocess
+import sys
+from pathlib import Path
 
 import numpy as np
 import pytest
@@ -129,3 +136,64 @@ def test_noalloc_refuses_plans_beyond_its_scratch(capi):
     assert status == 17, capi.xinfer_status_string(status)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())  # nothing was launched
+
+
+# Run in a fresh process, so that the entry point's first call -- the one that
+# looks up the scratch's device address -- happens inside the capture.
+CAPTURE_CHILD = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, sys.argv[2])
+from test_zz_no_alloc import host_offsets, view, case
+
+lib = ctypes.CDLL(sys.argv[1])
+lib.xinfer_status_string.restype = ctypes.c_char_p
+lib.xinfer_batched_flash_attention_workspace_size.restype = ctypes.c_size_t
+counts, lengths = [1, 1, 0, 1, 1, 1, 1, 1], [13312, 2162, 386, 9459, 1399, 3852, 55, 182]
+q, k, v = case(7, 8, 16, 8, 128, 16384, counts, lengths)
+qv, kv, vv = view(q), view(k), view(v)
+host = host_offsets(counts, lengths)
+scale = ctypes.c_double(128 ** -0.5)
+size = lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(qv), ctypes.byref(kv), host)
+assert size > 0
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(side):
+    # The workspace entry point first, eagerly: the expected result (and the
+    # kernels' first launches) before any capture.
+    workspace = torch.empty(size, dtype=torch.uint8, device="cuda")
+    expected = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
+    status = lib.xinfer_batched_flash_attention(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, scale,
+                                                ctypes.c_void_p(expected.data_ptr()),
+                                                ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size),
+                                                ctypes.c_void_p(side.cuda_stream))
+    assert status == 0, lib.xinfer_status_string(status)
+    out = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device="cuda")
+torch.cuda.current_stream().wait_stream(side)
+torch.cuda.synchronize()
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph):
+    status = lib.xinfer_batched_flash_attention_noalloc(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, scale, ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+assert status == 0, lib.xinfer_status_string(status)
+torch.cuda.synchronize()
+for replay in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    _ = torch.randn(1 << 20, device="cuda").sum()  # other eager work between replays
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), expected.view(torch.int16)), replay
+print("noalloc capture ok", flush=True)
+"""
+
+
+@torch.inference_mode()
+def test_noalloc_first_call_inside_graph_capture(library_path):
+    log("no-alloc: first call inside a graph capture (fresh process)")
+    tests = Path(__file__).resolve().parent
+    env = dict(os.environ, PYTHONPATH=os.pathsep.join(filter(None, [str(tests.parent), os.environ.get("PYTHONPATH")])))
+    result = subprocess.run([sys.executable, "-c", CAPTURE_CHILD, str(library_path), str(tests)],
+                            capture_output=True, text=True, timeout=300, env=env)
+    assert result.returncode == 0, result.stdout[-2000:] + result.stderr[-4000:]
+    assert "noalloc capture ok" in result.stdout

@@ -11,6 +11,13 @@
 // pointer as their split-record workspace, exactly as they receive a
 // caller-supplied workspace.
 //
+// The first call on a device may come while the caller's stream is being
+// captured into a HIP graph (the callers this entry point is for).  The
+// lookup enqueues no work, but the runtime may load the code object behind
+// it, which a capture in global or thread-local mode forbids; so this thread
+// switches to relaxed capture mode for the lookup alone and restores its mode
+// afterwards.
+//
 // Nothing in the array needs clearing between calls: every work item that
 // splits a query group writes each of its records (running max, sum and
 // unnormalised output) before the merge reads them, splits that see no key
@@ -37,8 +44,13 @@ hipError_t scratch_pointer(void **pointer) {
   std::lock_guard<std::mutex> lock(mutex);
   if (device_pointers[device] == nullptr) {
     void *address = nullptr;
-    status = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    status = hipThreadExchangeStreamCaptureMode(&mode);
     if (status != hipSuccess) return status;
+    status = hipGetSymbolAddress(&address, HIP_SYMBOL(scratch));
+    const hipError_t restored = hipThreadExchangeStreamCaptureMode(&mode);
+    if (status != hipSuccess) return status;
+    if (restored != hipSuccess) return restored;
     if (address == nullptr) return hipErrorInvalidSymbol;
     device_pointers[device] = address;
   }

@@ -1,4 +1,4 @@
-"""Write real tokens from padded rows into caller-owned KV buffers.
+"""In-place KV-cache append: each row's real new tokens go to their cache positions.
 
 Python entry of the native ``xinfer::append_kv_batched`` operator, with the
 reference's name and argument order (compiler/common/kernels/kv_cache.py:45-72).

@@ -12,7 +12,7 @@ from xinfer_amd.attention import load_attention_ops
 
 
 def projection_gemv(x, weight):
-    """Return F.linear-shaped output for one contiguous input row; no mutation.
+    """One input row times the weight's transpose, shaped as F.linear shapes it; inputs stay unchanged.
 
     ``x``: [1, ..., 1, k] with unit last stride; ``weight``: contiguous [n, k];
     both bf16 or both fp32, on one GPU.  Accumulates in fp32.  Invalid inputs
