@@ -84,7 +84,7 @@ struct Plan {
 // Measured prefill costs on one MI355X CU, for the planner's choice of split
 // size: one 64-key tile of a 128-vector item (D <= 128: 8 waves, two per
 // SIMD; D = 256: 4 waves), and an item's fixed prologue, fold and epilogue.
-double prefill_tile_us(int dp) { return dp <= 64 ? 0.9 : (dp <= 128 ? 1.15 : 3.2); }
+double prefill_tile_us(int dp) { return dp <= 64 ? 0.9 : (dp <= 128 ? 1.15 : 1.9); }
 constexpr double kPrefillItemUs = 4.5;
 // Merge launch: fixed cost, and the record read at about 5 TB/s.
 constexpr double kMergeLaunchUs = 5.0;

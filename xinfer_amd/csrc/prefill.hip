@@ -1,4 +1,5 @@
-// Chunked causal prefill attention on the gfx950 matrix cores (MFMA bf16).
+// Chunked causal prefill attention on the gfx950 matrix cores (MFMA bf16),
+// head dims up to 128 (padded to 64 or 128; head dim 256 is prefill_d256.hip).
 //
 // Replaces, for rows with more than 8 query vectors per KV head, the ATen
 // FlashAttention-2 calls of compiler/common/kernels/attention.cpp:66-72 and
@@ -9,8 +10,8 @@
 // vectors of one KV head are enumerated j = i*G + g (query i, grouped head g),
 // so one tile serves all G heads that share the K/V tile in LDS.
 //
-// Waves: four query groups of 32 vectors x KH.  With KH = 2 (head dims 64 and
-// 128) a block is 8 waves, two per SIMD, so one wave's MFMAs overlap the
+// Waves: four query groups of 32 vectors x KH = 2: a block is 8 waves, two
+// per SIMD, so one wave's MFMAs overlap the
 // other's softmax; waves w and w+4 (the same SIMD) take alternate 64-key tiles
 // of the item, each a whole tile, so a wave's per-tile softmax work (column
 // max, rescale test and rescale) is spent once per 64 keys and its two 32-key
@@ -29,18 +30,12 @@
 // fills one contiguous 1 KB block, and the lanes choose which 16-byte chunks of
 // the tile they fetch.  That choice implements an XOR swizzle of the chunks of
 // each key row (against LDS bank conflicts) with no address arithmetic on the
-// store side.  NST tiles are in flight: while tile t is computed, the loads of
-// tiles t+1 .. t+NST-1 are outstanding, with one barrier per tile.
+// store side.  Tiles go through a ring of four stages in two-tile windows:
+// while the window of tiles t, t+1 is computed, tiles t+2 and t+3 load.
 //
-// V is kept row-major ([key][d]) and read with ds_read_b64_tr_b16, which
-// transposes 4x16 blocks of 16-bit elements within each 16-lane group: lane j
-// supplies the address of V[k0 + j/4][d0 + 4(j%4) .. +3] and receives
-// V[k0 .. k0+3][d0 + j], i.e. four consecutive keys of one feature, which is
-// the A-operand layout of the PV product.
-//
-// MFMA 32x32x16 lane layout used (A: 32xK16, B: K16x32, C: 32x32):
-//   A lane l: row l%32, k = 8*(l/32) + 0..7      B lane l: col l%32, same k
-//   C lane l, reg r: row 8*(r/4) + 4*(l/32) + r%4, col l%32
+// V is kept row-major ([key][d]) and read with ds_read_b64_tr_b16 (the
+// transposing read of prefill_common.h), which gives the A-operand layout of
+// the PV product.  The MFMA lane layouts are in prefill_common.h.
 //
 // Softmax rescaling is exact: whenever a tile raises a column's running max m,
 // m becomes that tile max and the accumulator is rescaled (tiles that raise no
@@ -54,123 +49,34 @@
 // Several splits of a tile write fp32 partial records, combined by merge.hip;
 // a tile's records per split are laid out [D/4][128 vectors][4 features].
 // The tile-0 / split-0 item zeroes the row's padded queries (t >= count).
-#include "device_common.h"
-#include "kernel_args.h"
 #include "launch.h"
+#include "prefill_common.h"
 
 namespace xattn {
 
-constexpr int kTileQ = 128;  // query vectors per work item
-constexpr int kBN = 64;      // keys per LDS tile
+constexpr int kBN = 64;  // keys per LDS tile
 
-typedef short shortx4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-
-// Transposing 8-byte LDS read (see the header comment for the lane mapping).
-__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t *p) {
-  const shortx4 r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) shortx4 *)(p));
-  return __builtin_bit_cast(u32x2, r);
-}
-
-// One 16-byte-per-lane buffer load into LDS: lane i's 16 bytes land at LDS
-// byte address m0 + 16 * i.  Written as inline asm so that the compiler does
-// not track these loads: it would otherwise wait for all of them before any
-// transposing LDS read, which would drain the load pipeline every tile.  The
-// waits for them are explicit (wait_loads_and_barrier); loads the compiler
-// does track are unaffected, since extra outstanding loads only make its own
-// waits stricter.
-__device__ __forceinline__ void lds_load16(u32x4 rsrc, uint32_t lds_byte, uint32_t voffset, uint32_t soffset) {
-  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
-               :
-               : "s"(__builtin_amdgcn_readfirstlane(lds_byte)), "v"(voffset), "s"(rsrc),
-                 "s"(__builtin_amdgcn_readfirstlane(soffset))
-               : "memory", "m0");
-}
-
-// Buffer descriptor words for [base, base + bytes) (raw buffer, no stride;
-// loads past `bytes` return zero).
-__device__ __forceinline__ u32x4 buffer_words(const void *base, uint32_t bytes) {
-  const uint64_t p = reinterpret_cast<uint64_t>(base);
-  return u32x4{(uint32_t)p, (uint32_t)(p >> 32) & 0xffffu, bytes, 0x00020000u};
-}
-
-__device__ __forceinline__ uint32_t lds_address(const uint16_t *p) {
-  return (uint32_t)(uintptr_t)(lds_void *)(p);
-}
-
-// Wait until at most N vector-memory operations of this wave are outstanding
-// (loads return in issue order), then synchronise the block.  The empty asm
-// keeps the compiler from moving LDS accesses across the barrier.
-template <int N>
-__device__ __forceinline__ void wait_loads_and_barrier() {
-  static_assert(N >= 0 && N < 16, "vmcnt field");
-  // s_waitcnt encoding (gfx9): vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt_hi[15:14].
-  __builtin_amdgcn_s_waitcnt((N & 15) | (0x7 << 4) | (0xF << 8));
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Wait for this wave's LDS reads, then synchronise the block.
-__device__ __forceinline__ void wait_lds_and_barrier() {
-  __builtin_amdgcn_s_waitcnt((0xF) | (0x7 << 4) | (0x0 << 8) | (0x3 << 14));
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// Key range [ks0, ks1) of split `split` for a tile whose last visible key is kend-1.
-template <int BN>
-__device__ __forceinline__ void split_range(int kend, int nsplit, int split, int &ks0, int &ks1) {
-  const int per = ((kend + nsplit - 1) / nsplit + BN - 1) / BN * BN;
-  ks0 = min(kend, split * per);
-  ks1 = min(kend, ks0 + per);
-}
-
+// Head dims 64 and 128 (KH = 2: two waves per query group, 8 waves).
 template <int DP, int KH>
 struct PrefillShape {
+  static_assert(DP <= 128 && KH == 2, "head dims 64 and 128; head dim 256 is prefill_d256.hip");
   static constexpr int THREADS = 256 * KH;
   static constexpr int NDS = DP / 16;                 // k-steps of the QK product
   static constexpr int NDT = DP / 32;                 // 32-row d tiles of the output
   static constexpr int CHUNKS = DP / 8;               // 16-byte chunks per key row
-  // D = 256 (one wave per SIMD, 128 accumulator registers, 32-key tiles)
-  // stages the query tile in its own LDS region and keeps each wave's 64 Qᵀ
-  // operand registers in AGPRs, which MFMA reads as its B operand directly
-  // (the VGPRs hold the accumulators).
-  static constexpr bool QLDS = DP == 256;
-  static constexpr int BN = QLDS ? 32 : kBN;          // keys per tile
+  static constexpr int BN = kBN;                      // keys per tile
   static constexpr int TILE = BN * DP;                // bf16 elements of one K (or V) tile
   static constexpr int LOADS = BN * CHUNKS / THREADS;  // 16-byte loads per thread per K (or V) tile
-  static constexpr int QBYTES = QLDS ? kTileQ * DP * 2 : 0;  // resident query tile
-  // Tiles per barrier window (WIN) and LDS stages (K+V of a tile: 4*TILE
-  // bytes): two-tile windows over a ring of four stages when it fits in
-  // 128 KB, else one tile per barrier over a ring of as many stages as fit.
-  static constexpr int WIN = !QLDS && 4 * TILE * 4 <= 128 * 1024 ? 2 : 1;
-  static constexpr int NST = WIN == 2 ? 4 : (QLDS ? (160 * 1024 - QBYTES) / (4 * TILE) : (4 * TILE * 3 <= 100 * 1024 ? 3 : 2));
-  // KH = 2: the two waves of a query group take alternate tiles (ALT), each
-  // all BN keys of its tile.
-  static constexpr bool ALT = KH > 1;
-  static constexpr int KPW = ALT ? BN : BN / KH;      // keys of a tile each wave computes
+  // Two-tile windows over a ring of four stages (K+V of a tile: 4*TILE bytes).
+  static constexpr int NST = 4;
+  static_assert(NST * 4 * TILE <= 128 * 1024, "stages");
+  // The two waves of a query group take alternate tiles, each all BN keys of its tile.
+  static constexpr int KPW = BN;                      // keys of a tile each wave computes
   static constexpr int NKT = KPW / 32;                // 32-key sub-tiles per wave per tile
-  static constexpr int HALF_T = KH > 1 ? NDT / 2 : NDT;  // d tiles each wave finishes
-  static constexpr int FOLD = KH > 1 ? 8 * (HALF_T * 16 + 2) * 64 * 4 : 0;  // bytes of the key-slice fold
-  static constexpr int SMEM = (NST * 4 * TILE + QBYTES > FOLD ? NST * 4 * TILE + QBYTES : FOLD);
+  static constexpr int HALF_T = NDT / 2;              // d tiles each wave finishes
+  static constexpr int FOLD = 8 * (HALF_T * 16 + 2) * 64 * 4;  // bytes of the key-slice fold
+  static constexpr int SMEM = NST * 4 * TILE > FOLD ? NST * 4 * TILE : FOLD;
 };
-
-// XOR swizzles of the 16-byte chunks of a key row (chunk c of key k is stored
-// at slot c ^ swz(k)).  K: a K read takes chunk c of 32 consecutive keys, so
-// the 16 keys served together land in 16 different slots.  V: the 32 lanes
-// one LDS pass serves (8 bytes each) read chunks 4t .. 4t+3 of 4 consecutive
-// keys (k0 % 4 == 0); the swizzle moves each key's four chunks to its own
-// group of four slots, i.e. its own 16 of the 64 banks.  (With D = 64 two
-// rows share the banks, so keys k and k+1 already differ in bank half.)
-template <int CHUNKS>
-__device__ __forceinline__ int k_swizzle(int key) { return key & (CHUNKS >= 16 ? 15 : CHUNKS - 1); }
-template <int CHUNKS>
-__device__ __forceinline__ int v_swizzle(int key) { return CHUNKS >= 16 ? 4 * (key & 3) : 4 * ((key >> 1) & 1); }
 
 template <int DP, int KH>
 __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
@@ -214,15 +120,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int b = rs.batch, L = rs.length, cnt = rs.count;
   const int qrows = cnt * G, p0 = L - cnt;
 
-  if (tile == 0 && split == 0 && cnt < T) {  // zero the row's padded queries
-    const int chunks = D / 8, per = (T - cnt) * chunks;
-    for (int idx = tid; idx < G * per; idx += THREADS) {
-      const int g = idx / per, rest = idx - g * per;
-      const int t = cnt + rest / chunks, ch = rest - (rest / chunks) * chunks;
-      store16(a.out + b * a.o_sb + (int64_t)(h * G + g) * a.o_sh + (int64_t)t * a.o_st + ch * 8,
-              u32x4{0, 0, 0, 0});
-    }
-  }
+  if (tile == 0 && split == 0 && cnt < T) zero_padded_queries(a, b, h, cnt, G, D, T, tid, THREADS);
 
   // Key range of this tile and split.
   const int j_last = min(tile * kTileQ + kTileQ, qrows) - 1;
@@ -264,9 +162,8 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // holds query vector j, swizzled like K.  Rows past the tile's queries and
   // features past D load as zero (an offset past the descriptor's range).
   constexpr int QLOADS = kTileQ * CHUNKS / THREADS;
-  static_assert(kTileQ * CHUNKS == QLOADS * THREADS && (S::QLDS || kTileQ * DP <= 2 * TILE),
-                "query tile fits a stage");
-  uint16_t *const qtile = smem + (S::QLDS ? NST * 2 * TILE : (NST - 1) * 2 * TILE);
+  static_assert(kTileQ * CHUNKS == QLOADS * THREADS && kTileQ * DP <= 2 * TILE, "query tile fits a stage");
+  uint16_t *const qtile = smem + (NST - 1) * 2 * TILE;
   auto issue_query = [&]() {
     const u32x4 q_rsrc = buffer_words(qv.p + b * qv.sb + (int64_t)(h * G) * qv.sh, 0x7fffffffu);
     uint16_t *qdst = qtile;
@@ -292,12 +189,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   };
 
   // LDS read offsets (elements) of this lane, fixed for the whole item.
-  // K (A operand of QK): key kl = kbase + 32kt + col, chunk 2ds + half, with
-  // kbase the first key of the wave's share of a tile (0 when the waves of a
-  // query group alternate tiles).
+  // K (A operand of QK): key kl = 32kt + col, chunk 2ds + half.
   // Q (B operand, read once): row jr = qgroup*32 + col, same chunks.
-  const int kbase = S::ALT ? 0 : khalf * KPW;
-  const int kl0 = kbase + col, jr0 = qgroup * 32 + col;
+  const int kl0 = col, jr0 = qgroup * 32 + col;
   int k_off[NDS];
 #pragma unroll
   for (int ds = 0; ds < NDS; ++ds) k_off[ds] = kl0 * DP + (((2 * ds + half) ^ k_swizzle<CHUNKS>(kl0)) * 8);
@@ -305,7 +199,7 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // addresses key kv0 (+16hh +8 for the second read) and features
   // 32t + 16(gq%2) + 4(jj%4); kv0 % 4 == jj / 4 for every read.
   const int gq = lane >> 4, jj = lane & 15;
-  const int kv0 = kbase + 4 * (gq >> 1) + (jj >> 2);
+  const int kv0 = 4 * (gq >> 1) + (jj >> 2);
   int v_off[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) {
@@ -324,47 +218,22 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   bf16x8 qf[NDS];  // Q^T B operands, read from LDS at tile 0
   auto compute = [&](int stage, int kb) {
     const uint16_t *Kt = smem + stage * 2 * TILE, *Vt = Kt + TILE;
-    const int kw = kb + kbase;  // first key of this wave's share
+    const int kw = kb;  // first key of this wave's tile
     if (!(wave_active && kw <= wave_kmax && kw < ks1)) return;
     f32x16 s[NKT];
-    if constexpr (S::QLDS) {
-      // Qᵀ operands from AGPRs (read at tile 0); K operands from LDS in groups
-      // of two k-steps, one group ahead of the MFMAs, and the scheduler may
-      // not hoist further: the 128 accumulator registers leave no room for
-      // more.  Measured on cfg5: 546.8 -> 539.2 us against Qᵀ read from LDS
-      // next to each K operand (a third of the tile's LDS reads).
-      static_assert(KH == 1 && NKT == 1, "D = 256 layout: one key slice of 32-key tiles");
-      constexpr int GR = 2;
-      u32x4 ka[2][GR];
-      auto load = [&](int g, int buf) {
+    // The NKT 32-key blocks are independent accumulation chains; k-step
+    // outer, so their MFMAs alternate.
 #pragma unroll
-        for (int u = 0; u < GR; ++u) ka[buf][u] = *reinterpret_cast<const u32x4 *>(Kt + k_off[g * GR + u]);
-      };
+    for (int kt = 0; kt < NKT; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) s[0][r] = 0.0f;
-      load(0, 0);
+      for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
 #pragma unroll
-      for (int g = 0; g < NDS / GR; ++g) {
-        if (g + 1 < NDS / GR) load(g + 1, (g + 1) & 1);
+    for (int ds = 0; ds < NDS; ++ds)
 #pragma unroll
-        for (int u = 0; u < GR; ++u) s[0] = mfma32(as_bf16x8(ka[g & 1][u]), qf[g * GR + u], s[0]);
-        __builtin_amdgcn_sched_barrier(0);
+      for (int kt = 0; kt < NKT; ++kt) {
+        const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
+        s[kt] = mfma32(ka, qf[ds], s[kt]);
       }
-    } else {
-      // The NKT 32-key blocks are independent accumulation chains; k-step
-      // outer, so their MFMAs alternate.
-#pragma unroll
-      for (int kt = 0; kt < NKT; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) s[kt][r] = 0.0f;
-#pragma unroll
-      for (int ds = 0; ds < NDS; ++ds)
-#pragma unroll
-        for (int kt = 0; kt < NKT; ++kt) {
-          const bf16x8 ka = as_bf16x8(*reinterpret_cast<const u32x4 *>(Kt + k_off[ds] + kt * 32 * DP));
-          s[kt] = mfma32(ka, qf[ds], s[kt]);
-        }
-    }
     // Mask keys past this column's causal limit or past the split.
     if (kw + KPW - 1 > wave_kmin || kw + KPW > ks1) {
 #pragma unroll
@@ -414,35 +283,6 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     // O^T += V^T P^T.  B element e of k-step (kt, hh) is S^T register hh*8+e:
     // key 32kt + 16hh + 8(e/4) + 4half + e%4, i.e. two runs of 4 keys, which the
     // two transposing reads of each A operand supply.
-    if constexpr (S::QLDS) {
-      // V operands one d tile ahead of its MFMAs.  Measured on cfg5 (same
-      // outputs): groups of one d tile 504 us, of two 516 us, of four 503 us,
-      // all eight at once 526 us.
-      constexpr int GT = 1;
-      u32x4 va[2][GT][2];
-      auto load = [&](int g, int buf) {
-#pragma unroll
-        for (int u = 0; u < GT; ++u)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            const uint16_t *vp = Vt + v_off[g * GT + u] + hh * 16 * DP;
-            const u32x2 lo = lds_read_tr16(vp), hi = lds_read_tr16(vp + 8 * DP);
-            va[buf][u][hh] = u32x4{lo.x, lo.y, hi.x, hi.y};
-          }
-      };
-      load(0, 0);
-#pragma unroll
-      for (int g = 0; g < NDT / GT; ++g) {
-        if (g + 1 < NDT / GT) load(g + 1, (g + 1) & 1);
-#pragma unroll
-        for (int u = 0; u < GT; ++u)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
-            acc[g * GT + u] = mfma32(as_bf16x8(va[g & 1][u][hh]), pb[0][hh], acc[g * GT + u]);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      return;
-    }
     // V operands one d tile ahead of their MFMAs (measured on cfg2, same
     // outputs: 21.2 against 21.5 us with the reads left to the scheduler;
     // K operands one k-step ahead in the score loop measured slower).
@@ -471,21 +311,14 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
 
   // Pipeline.  The query tile is read into registers at tile 0, after which
   // a second barrier frees its buffer (the last stage).
-  constexpr int PER_TILE = 2 * LOADS;  // load instructions per tile per thread
   auto read_query = [&]() {
 #pragma unroll
     for (int ds = 0; ds < NDS; ++ds)
       qf[ds] = as_bf16x8(*reinterpret_cast<const u32x4 *>(qtile + jr0 * DP +
                                                            (((2 * ds + half) ^ k_swizzle<CHUNKS>(jr0)) * 8)));
-    if constexpr (S::QLDS) {
-      // One wave per SIMD leaves the AGPRs free: the Qᵀ operands live there
-      // for the item (MFMA reads its B operand from AGPRs directly).
-#pragma unroll
-      for (int ds = 0; ds < NDS; ++ds) asm volatile("" : "+a"(qf[ds]));
-    }
     wait_lds_and_barrier();
   };
-  if constexpr (S::WIN == 2) {
+  {
     // Two-tile windows over four stages: at the start of the window of tiles
     // t, t+1 wait for their loads and synchronise (every wave is done with
     // tiles t-2 and t-1), refill those two stages with tiles t+2, t+3, then
@@ -506,38 +339,8 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
           if (t == 0) read_query();
           if (t + 2 < ntile) issue((2 * w + 2) % 4, ks0 + (t + 2) * BN);
           if (t + 3 < ntile) issue((2 * w + 3) % 4, ks0 + (t + 3) * BN);
-          static_assert(S::ALT, "two-tile windows: the waves of a query group alternate tiles");
           if (khalf == 0) compute(2 * w, ks0 + t * BN);
           else if (t + 1 < ntile) compute(2 * w + 1, ks0 + (t + 1) * BN);
-        }
-      }
-    }
-  } else {
-    // One tile per barrier: before computing tile t, wait for its loads (the
-    // loads of tiles t+1 .. t+NST-2 may stay outstanding), barrier (the tile
-    // is complete in LDS and every wave has finished tile t-1), then refill
-    // the stage of tile t-1 with tile t+NST-1.
-    if (ntile > 0) {
-      issue_query();
-#pragma unroll
-      for (int st = 0; st < NST - 1; ++st)
-        if (st < ntile) issue(st, ks0 + st * BN);
-    }
-    for (int t0 = 0; t0 < ntile; t0 += NST) {
-#pragma unroll
-      for (int st = 0; st < NST; ++st) {
-        const int t = t0 + st;
-        if (t < ntile) {
-          const int ahead = min(ntile - 1 - t, NST - 2);  // tiles after t already issued
-          if constexpr (NST == 3) {
-            if (ahead >= 1) wait_loads_and_barrier<PER_TILE>();
-            else wait_loads_and_barrier<0>();
-          } else {
-            wait_loads_and_barrier<0>();
-          }
-          if (t == 0) read_query();
-          if (t + NST - 1 < ntile) issue((st + NST - 1) % NST, ks0 + (t + NST - 1) * BN);
-          compute(st, ks0 + t * BN);
         }
       }
     }
@@ -625,15 +428,6 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   }
 }
 
-// The D = 256 kernel is built in its own translation unit (prefill_d256.hip
-// includes this file with XATTN_PREFILL_D256 defined), so that it can take
-// its own scheduler flags.
-#ifdef XATTN_PREFILL_D256
-hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t stream) {
-  hipLaunchKernelGGL((prefill_kernel<256, 1>), dim3(blocks), dim3(256), 0, stream, a);
-  return hipGetLastError();
-}
-#else
 // Blocks per launch: 8 times the longest XCD run (blocks past their run exit
 // at once).
 hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream) {
@@ -650,6 +444,5 @@ hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream) {
   }
   return hipGetLastError();
 }
-#endif
 
 }  // namespace xattn
