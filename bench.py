@@ -78,15 +78,18 @@ def sources_digest():
 def dominant_kernel(w):
     """Name of the kernel that carries the workload's algorithmic work.
 
-    Mirrors the library's kernel choice: head dims pad to 64 / 128 / 256; prefill
-    uses two waves per query group (8 waves) at 128; decode is instantiated
-    for the power-of-two query vectors per KV head (count * G) and the rounds
-    per item, four when one-round items would number at least 1536 (the
-    planner in capi.cpp), else one.
+    Mirrors the library's kernel choice: head dims pad to 64 / 128 / 256;
+    prefill runs two waves per query group (8 waves) at 64 and 128 and the
+    kernel of its own at 256 (a plain function, so its demangled name carries
+    no return type); decode is instantiated for the power-of-two query vectors
+    per KV head (count * G) and the rounds per item, four when one-round items
+    would number at least 1536 (the planner in capi.cpp), else one.
     """
     dp = 64 if w.dim <= 64 else (128 if w.dim <= 128 else 256)
     if w.kind == "prefill":
-        return f"void xattn::prefill_kernel<{dp}, {2 if dp == 128 else 1}>(xattn::AttnArgs)"
+        if dp == 256:
+            return "xattn::prefill_d256_kernel(xattn::AttnArgs)"
+        return f"void xattn::prefill_kernel<{dp}, 2>(xattn::AttnArgs)"
     group = w.heads // w.kv_heads
     qv = max(1, max(c for c in w.counts) * group)
     qr = 1
@@ -127,7 +130,7 @@ def record_traffic(fetch_csv, write_csv):
         scale = COPY_PROBE_BYTES / (averages[probes[0]] * 1024)
         record[counter.lower() + "_scale"] = scale
         for name, kib in averages.items():
-            if name.startswith("void xattn::"):
+            if name.startswith(("void xattn::", "xattn::")):
                 entry = record["kernels"].setdefault(name, {})
                 entry[counter.lower() + "_kib"] = kib
                 entry[counter.lower() + "_bytes"] = kib * 1024 * scale
