@@ -1,0 +1,314 @@
+"""Whole model steps with native attention layers: export, package, fresh-process runs.
+
+Counterpart of compiler/qwen3/tests/test_export.py:60-180 (the model step
+exported with batch in [1, 8] and prefill tokens in [2, 512]; one
+batched_flash_attention and one append per layer, no index_copy, no SDPA, no
+mutated buffers; the exported module equal to the eager step bit for bit for
+B = 1..8 over ragged count patterns with inactive rows; cache slots outside
+each append untouched; B = 0 and B = 9 refused) and of
+compiler/qwen35/tests/test_export.py:161-175 (the same counts for Qwen3.5's
+gated full-attention layers), carried on through ``compile_package`` into
+fresh processes.
+
+Three steps (``xinfer_amd.adapters.ModelStep``), each a two-layer model built
+from transformers' own classes with random weights (``model_steps``): Qwen3
+with the reference adapter's sequence, Qwen3 with the fused
+``qk_norm_rope_append`` + ``batched_flash_attention_bthd`` form, and Qwen3.5
+with its gated attention.  Each is exported for prefill and decode and
+packaged with the library as constants-in-package (weights inside the .so).
+
+A fresh process that never loads the build tree's library takes the library
+out of the packages, rebuilds the eager step and the unmodified transformers
+model from the saved weights, and for B = 1..8 over the reference's patterns
+checks:
+
+* package against eager: cache slots outside each row's append bit for bit
+  unchanged; rows without tokens give zero logits; each row's logits within
+  relative L2 2e-2 and peak relative error 3e-2, its appended K/V within
+  relative L2 1e-2.  Bits are not required here: the native operators and the
+  projection GEMMs (extern calls to the same library routines) are the same
+  code in both, but Inductor writes its own kernels for the RMSNorms, the
+  rotary tables, SiLU and the sigmoid gate, whose fp32 reductions and
+  transcendentals round a few elements differently from the ATen kernels
+  eager runs, and a flipped bf16 element of one layer moves everything after
+  it.  The process reports how many logits rows and appended slots came out
+  identical (on MI355X: 185, 188 and 159 of 196 rows, 99.98 %, 99.98 % and
+  99.5 % of the slots; worst logits row 0.44 %, 0.45 % and 0.78 % relative
+  L2);
+* for B = 1, 3 and 8: the unmodified transformers model, row by row, within
+  the reference's layer bounds (relative L2 and peak relative error 0.05 on
+  the logits, compiler/qwen3/tests/test_attention.py:157-160), and its
+  index_copy_ cache against the package's appended slots: layer 0 within the
+  reference's append bound (relative L2 1e-2), layer 1, whose K/V are
+  computed from layer 0's output, within 2e-2.
+"""
+
+import json
+import os
+from pathlib import Path
+import subprocess
+import sys
+import textwrap
+
+import pytest
+import torch
+from torch.fx.experimental import _config as symbolic_config
+
+from attn_helpers import log
+from model_steps import CAPACITY, LAYERS, VARIANTS, build_model, step_inputs
+
+pytestmark = pytest.mark.gpu
+
+ROOT = Path(__file__).resolve().parents[1]
+PATTERNS = {"decode": ((1,), (0, 1), (1, 0)), "prefill": ((7, 16), (1, 2), (0, 16), (512, 1))}
+
+
+def export_step(step, kind):
+    """Export one entry point as the reference's exporter does (compiler/qwen3/export.py:27-56)."""
+    batch_size, width = 2, (1 if kind == "decode" else 16)
+    kv_heads, dim = step.model.config.num_key_value_heads, step.model.config.head_dim
+    cache = tuple(torch.zeros(batch_size, kv_heads, CAPACITY, dim, device="cuda", dtype=torch.bfloat16)
+                  for _ in range(2 * LAYERS))
+    starts = [16 + 8 * row for row in range(batch_size)]
+    counts = [max(1, width // (row + 1)) for row in range(batch_size)]
+    inputs = (torch.ones((batch_size, width), dtype=torch.int64, device="cuda"),
+              torch.stack([torch.arange(start, start + width, device="cuda") for start in starts]),
+              cache,
+              torch.tensor([start + count for start, count in zip(starts, counts)], dtype=torch.int32),
+              torch.tensor(counts, dtype=torch.int32))
+    batch = torch.export.Dim("batch", min=1, max=8)
+    token_shape = {0: batch}
+    if kind == "prefill":
+        token_shape[1] = torch.export.Dim("tokens", min=2, max=512)
+    shapes = (token_shape, token_shape, tuple({0: batch} for _ in cache), {0: batch}, {0: batch})
+    with symbolic_config.patch(backed_size_oblivious=True):
+        exported = torch.export.export(step, inputs, dynamic_shapes=shapes, strict=False)
+    exported.validate()
+    return exported
+
+
+@pytest.fixture(scope="module", params=list(VARIANTS))
+def bundle(request, gpu_ops, tmp_path_factory):
+    from xinfer_amd.adapters import ModelStep
+    from xinfer_amd.attention import attention_c_shims, attention_library
+    from xinfer_amd.package import compile_package
+
+    name = request.param
+    family, fused = VARIANTS[name]
+    directory = tmp_path_factory.mktemp(name)
+    model = build_model(family)
+    torch.save({key: value.cpu() for key, value in model.state_dict().items()}, directory / "weights.pt")
+    step = ModelStep(model, fused=fused)
+    programs = {}
+    for kind in ("prefill", "decode"):
+        log(f"export + AOTI package of the {name} {kind} step")
+        with torch.inference_mode():
+            program = export_step(step, kind)
+            compile_package(program, directory / f"{kind}.pt2", inductor_configs={"emulate_precision_casts": True},
+                            native_libraries=[Path(attention_library())], custom_op_shims=attention_c_shims())
+        programs[kind] = program
+    return name, directory, step, programs
+
+
+def test_exported_steps_hold_one_attention_and_one_append_per_layer(bundle, gpu_ops):
+    name, _, step, programs = bundle
+    fused = VARIANTS[name][1]
+    attention = gpu_ops.batched_flash_attention_bthd.default if fused else gpu_ops.batched_flash_attention.default
+    append = gpu_ops.qk_norm_rope_append.default if fused else gpu_ops.append_kv_batched.default
+    others = {gpu_ops.batched_flash_attention.default, gpu_ops.batched_flash_attention_bthd.default,
+              gpu_ops.append_kv_batched.default, gpu_ops.qk_norm_rope_append.default} - {attention, append}
+    for kind, program in programs.items():
+        log(f"exported graph {name} {kind}")
+        ids = next(node for node in program.graph.nodes if node.op == "placeholder" and node.target == "input_ids")
+        constraint = program.range_constraints[ids.meta["val"].shape[0].node.expr]
+        assert (constraint.lower, constraint.upper) == (1, 8)
+        if kind == "prefill":
+            constraint = program.range_constraints[ids.meta["val"].shape[1].node.expr]
+            assert (constraint.lower, constraint.upper) == (2, 512)
+        assert not program.graph_signature.buffers_to_mutate
+        targets = [node.target for node in program.graph.nodes if node.op == "call_function"]
+        assert targets.count(attention) == LAYERS and targets.count(append) == LAYERS
+        assert not any(targets.count(op) for op in others)
+        assert torch.ops.aten.index_copy.default not in targets
+        assert torch.ops.aten.index_copy_.default not in targets
+        assert torch.ops.aten.scaled_dot_product_attention.default not in targets
+
+
+@torch.inference_mode()
+def test_exported_step_equals_eager_for_every_batch(bundle):
+    """compiler/qwen3/tests/test_export.py:98-155: the exported module against the eager step, bit for bit."""
+    name, _, step, programs = bundle
+    for kind, program in programs.items():
+        exported = program.module()
+        cases = 0
+        for batch in range(1, 9):
+            for pattern in PATTERNS[kind]:
+                counts = [pattern[row % len(pattern)] for row in range(batch)]
+                if not max(counts):
+                    continue
+                log(f"exported {name} {kind}: batch={batch} counts={counts}")
+                ids, positions, initial, lengths, queries, starts = step_inputs(step.model, kind, counts,
+                                                                                seed=100 * batch + cases)
+                results = []
+                for call in (step, exported):
+                    state = tuple(t.clone() for t in initial)
+                    logits = call(ids, positions, tuple(t[:batch] for t in state), lengths, queries)
+                    results.append((logits, state))
+                    assert bool(torch.isfinite(logits).all())
+                    for row, count in enumerate(counts):
+                        if count == 0:
+                            assert torch.count_nonzero(logits[row]).item() == 0
+                    for before, after in zip(initial, state):
+                        assert torch.equal(before[batch:], after[batch:])
+                        for row, (start, count) in enumerate(zip(starts, counts)):
+                            assert torch.equal(before[row, :, :start], after[row, :, :start])
+                            assert torch.equal(before[row, :, start + count:], after[row, :, start + count:])
+                (eager, eager_state), (program_out, program_state) = results
+                assert torch.equal(eager, program_out), (name, kind, batch, counts)
+                assert all(torch.equal(a, b) for a, b in zip(eager_state, program_state))
+                cases += 1
+        for batch in (0, 9):
+            width = 1 if kind == "decode" else 2
+            kv_heads, dim = step.model.config.num_key_value_heads, step.model.config.head_dim
+            bad = (torch.ones((batch, width), dtype=torch.int64, device="cuda"),
+                   torch.zeros((batch, width), dtype=torch.int64, device="cuda"),
+                   tuple(torch.zeros(batch, kv_heads, CAPACITY, dim, device="cuda", dtype=torch.bfloat16)
+                         for _ in range(2 * LAYERS)),
+                   torch.ones(batch, dtype=torch.int32), torch.ones(batch, dtype=torch.int32))
+            try:
+                logits = exported(*bad)
+            except (RuntimeError, AssertionError, ValueError):
+                continue
+            # This PyTorch's guards do not enforce the lower bound: B = 0 may
+            # run, and must then return no rows.
+            assert batch == 0, f"batch {batch} accepted by the exported {name} {kind} step"
+            assert logits.shape[0] == 0
+
+
+WORKER = textwrap.dedent(
+    """
+    import json, sys
+    from pathlib import Path
+    sys.path.insert(0, sys.argv[1])
+    sys.path.insert(0, str(Path(sys.argv[1]) / 'tests'))
+    import torch
+    from xinfer_amd.validation import load_packaged_attention_ops
+    from xinfer_amd.adapters import ModelStep
+    from xinfer_amd.package import load_package
+    from model_steps import VARIANTS, build_model, step_inputs, transformers_row_logits
+
+    directory, build_library, name = Path(sys.argv[2]), Path(sys.argv[3]), sys.argv[4]
+    PATTERNS = {'decode': ((1,), (0, 1), (1, 0)), 'prefill': ((7, 16), (1, 2), (0, 16), (512, 1))}
+    family, fused = VARIANTS[name]
+    extracted = load_packaged_attention_ops(directory)
+    state = torch.load(directory / 'weights.pt', weights_only=True)
+    step = ModelStep(build_model(family, state), fused=fused)
+    plain = build_model(family, state)
+    packages = {kind: load_package(directory / f'{kind}.pt2') for kind in ('prefill', 'decode')}
+
+    def errors(actual, expected):
+        delta = (actual.float() - expected.float()).flatten(1)
+        ref = expected.float().flatten(1)
+        return dict(relative_l2=float((delta.norm(dim=-1) / ref.norm(dim=-1).clamp_min(1e-12)).max()),
+                    peak_relative=float((delta.abs().amax(dim=-1) / ref.abs().amax(dim=-1).clamp_min(1e-12)).max()))
+
+    report = dict(cases=0, rows=0, identical_rows=0, appended_slots=0, identical_slots=0,
+                  package_vs_eager=dict(relative_l2=0.0, peak_relative=0.0), kv_vs_eager=0.0,
+                  transformers_rows=0, package_vs_transformers=dict(relative_l2=0.0, peak_relative=0.0),
+                  kv_vs_transformers=[0.0] * (len(step.model.model.layers)))
+
+    def worst(entry, found):
+        for key, value in found.items():
+            entry[key] = max(entry[key], value)
+
+    with torch.inference_mode():
+        for kind, package in packages.items():
+            for batch in range(1, 9):
+                for pattern in PATTERNS[kind]:
+                    counts = [pattern[row % len(pattern)] for row in range(batch)]
+                    if not max(counts):
+                        continue
+                    case = f'{name} {kind} batch={batch} counts={counts}'
+                    print(case, file=sys.stderr, flush=True)
+                    ids, positions, initial, lengths, queries, starts = step_inputs(
+                        step.model, kind, counts, seed=1000 * batch + report['cases'])
+                    results = []
+                    for call in (step, package):
+                        kv = tuple(t.clone() for t in initial)
+                        logits = call(ids, positions, tuple(t[:batch] for t in kv), lengths, queries)
+                        results.append((logits, kv))
+                    torch.cuda.synchronize()
+                    (eager, eager_kv), (packaged, package_kv) = results
+                    if not bool(torch.isfinite(packaged).all()):
+                        raise AssertionError(f'nonfinite package logits: {case}')
+                    for before, after in zip(initial, package_kv):
+                        if not torch.equal(before[batch:], after[batch:]):
+                            raise AssertionError(f'rows past the batch changed: {case}')
+                        for row, (start, count) in enumerate(zip(starts, counts)):
+                            if not (torch.equal(before[row, :, :start], after[row, :, :start])
+                                    and torch.equal(before[row, :, start + count:], after[row, :, start + count:])):
+                                raise AssertionError(f'cache slot outside the append changed: {case}')
+                    for row, (start, count) in enumerate(zip(starts, counts)):
+                        if count == 0:
+                            if torch.count_nonzero(packaged[row]).item():
+                                raise AssertionError(f'row without tokens has logits: {case}')
+                            continue
+                        report['rows'] += 1
+                        report['identical_rows'] += bool(torch.equal(packaged[row], eager[row]))
+                        found = errors(packaged[row:row + 1], eager[row:row + 1])
+                        if found['relative_l2'] > 2e-2 or found['peak_relative'] > 3e-2:
+                            raise AssertionError(f'package and eager logits beyond the bounds: {case} row {row} {found}')
+                        worst(report['package_vs_eager'], found)
+                        for mine, theirs in zip(package_kv, eager_kv):
+                            slots, other = mine[row, :, start:start + count], theirs[row, :, start:start + count]
+                            kv_error = errors(slots.flatten()[None], other.flatten()[None])['relative_l2']
+                            if kv_error > 1e-2:
+                                raise AssertionError(f'package and eager K/V beyond the bound: {case} row {row} {kv_error}')
+                            report['kv_vs_eager'] = max(report['kv_vs_eager'], kv_error)
+                            report['appended_slots'] += slots.numel()
+                            report['identical_slots'] += int((slots.view(torch.int16) == other.view(torch.int16)).sum())
+                        if batch in (1, 3, 8):
+                            tensors = tuple(t[row:row + 1].clone() for t in initial)
+                            position = positions[row:row + 1, :count]
+                            expected = transformers_row_logits(plain, ids[row:row + 1, :count], position, tensors)
+                            found = errors(packaged[row:row + 1], expected)
+                            if found['relative_l2'] > 0.05 or found['peak_relative'] > 0.05:
+                                raise AssertionError(f'package outside the transformers bounds: {case} row {row} {found}')
+                            worst(report['package_vs_transformers'], found)
+                            for index, (mine, theirs) in enumerate(zip(package_kv, tensors)):
+                                layer = index // 2
+                                kv_error = errors(mine[row, :, start:start + count].flatten()[None],
+                                                  theirs[0, :, start:start + count].flatten()[None])['relative_l2']
+                                if kv_error > (1e-2 if layer == 0 else 2e-2):
+                                    raise AssertionError(f'layer {layer} K/V outside the bound: {case} row {row} {kv_error}')
+                                report['kv_vs_transformers'][layer] = max(report['kv_vs_transformers'][layer], kv_error)
+                            report['transformers_rows'] += 1
+                    report['cases'] += 1
+    paths = {line.split(maxsplit=5)[5].removesuffix(' (deleted)')
+             for line in Path('/proc/self/maps').read_text().splitlines() if 'libxinfer_attention_ops.so' in line}
+    if len(paths) != 1:
+        raise AssertionError(f'expected one mapped attention library: {paths}')
+    library = paths.pop()
+    if Path(library) == build_library or Path(library) != Path(extracted):
+        raise AssertionError(f'not the packaged library: {library}')
+    report['library'] = library
+    print(json.dumps(report), flush=True)
+    """
+)
+
+
+def test_packaged_step_in_a_fresh_process(bundle):
+    from xinfer_amd.attention import attention_library
+
+    name, directory, _, _ = bundle
+    env = dict(os.environ, XINFER_ATTENTION_OPS_LIBRARY="/nonexistent/attention.so")
+    env.pop("PYTHONPATH", None)
+    log(f"fresh process, {name} model-step packages")
+    result = subprocess.run([sys.executable, "-c", WORKER, str(ROOT), str(directory), str(attention_library()), name],
+                            env=env, capture_output=True, text=True, timeout=900)
+    assert result.returncode == 0, result.stdout[-4000:] + result.stderr[-4000:]
+    report = json.loads(result.stdout.splitlines()[-1])
+    log(f"{name}: {json.dumps(report)}")
+    # Every pattern at every batch, less the all-inactive one-row batches.
+    assert report["cases"] == (3 * 8 - 1) + (4 * 8 - 1)
+    assert report["transformers_rows"] > 0
