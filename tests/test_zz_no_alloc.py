@@ -2,11 +2,13 @@
 
 xinfer_batched_flash_attention_noalloc runs the same plan and kernels as
 xinfer_batched_flash_attention, with the split records in the library's
-static device scratch instead of a caller's workspace.  Two calls in a row --
-a 512-token prefill chunk whose records fill half of the scratch, then a
-smaller ragged decode batch -- must each equal the workspace entry point bit
-for bit (the second call finds the first call's records in the scratch and
-must not depend on them), and stay within the oracle gates.  A plan beyond
+static device scratch instead of a caller's workspace.  Three calls in a row
+-- a 512-token prefill chunk whose records fill half of the scratch, a
+smaller ragged decode batch, and a short-row decode batch whose splits the
+decode launch merges itself, with its arrival counters in the scratch -- must
+each equal the workspace entry point bit for bit (each call finds the earlier
+calls' records in the scratch and must not depend on them), and stay within
+the oracle gates.  A plan beyond
 the scratch is refused before any launch.  In a fresh process, the first
 call (which looks up the scratch's device address) is made while a HIP graph
 is being captured; every replay of that graph must equal the workspace entry
@@ -102,7 +104,7 @@ def check_oracle(out, q, k, v, counts, lengths, scale):
 
 
 @torch.inference_mode()
-def test_noalloc_equals_the_workspace_entry_point_on_two_calls(capi):
+def test_noalloc_equals_the_workspace_entry_point_on_three_calls(capi):
     # First call: a 512-token chunk at offset 1536 (records fill half the scratch).
     counts, lengths = [512], [2048]
     log(f"no-alloc call 1: prefill counts={counts} lengths={lengths}")
@@ -119,6 +121,15 @@ def test_noalloc_equals_the_workspace_entry_point_on_two_calls(capi):
     assert 0 < size2 < size
     assert torch.equal(out2.view(torch.int16), expected2.view(torch.int16))
     check_oracle(out2, q, k, v, counts, lengths, 128**-0.5)
+    # Third call: a short-row decode batch whose splits the decode launch
+    # merges itself (arrival counters in the scratch, past the records).
+    counts, lengths = [1, 1, 1], [1024, 700, 900]
+    log(f"no-alloc call 3: decode counts={counts} lengths={lengths}")
+    q, k, v = case(8, 3, 16, 8, 128, 2048, counts, lengths)
+    out3, expected3, size3 = run_both(capi, q, k, v, counts, lengths, 128**-0.5)
+    assert 0 < size3 < size2
+    assert torch.equal(out3.view(torch.int16), expected3.view(torch.int16))
+    check_oracle(out3, q, k, v, counts, lengths, 128**-0.5)
 
 
 @torch.inference_mode()

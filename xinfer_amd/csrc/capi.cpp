@@ -4,13 +4,18 @@
 // kernel arguments (kernel_args.h): rows with at most 8 query vectors per KV
 // head go to the split-KV decode kernel, the others to the MFMA prefill
 // kernel; rows whose keys are split get fp32 partial records in the caller's
-// workspace, combined by a merge launch after the attention kernels.  The
-// schedule is a function of the shapes and lengths only, never of tensor data,
-// so results are deterministic and each row is isolated from the others'
-// contents.
+// workspace, combined by a merge launch after the attention kernels or, for
+// small decode launches, by the last split of each (row, kv head) inside the
+// decode launch (decode.hip: merge_in_launch), which folds in the merge
+// launch's order and arithmetic.  The schedule is a function of the shapes and
+// lengths only, never of tensor data, so results are deterministic and each
+// row is isolated from the others' contents.
 #include <algorithm>
+#include <atomic>
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
+#include <mutex>
 #include <vector>
 
 #include "xinfer_attention.h"
@@ -71,14 +76,21 @@ struct Group {
   int pre_items = 0;
   MergeArgs merge{};
   int merge_items = 0, merge_max_splits = 0;
+  // The decode launch may merge its split rows itself (decode_merge_fusable).
+  bool dec_fusable = false;
 };
 
 struct Plan {
   std::vector<Group> groups;
   int64_t records = 0;
   int64_t D = 0;
+  // Arrival counters of the decode in-launch merge: one per decode item of
+  // the largest fusable group (the groups' launches run one after another and
+  // leave every counter at zero).
+  int64_t counters = 0;
   size_t part_ml_offset() const { return (size_t)((records * D * 4 + 255) / 256 * 256); }
-  size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
+  size_t counters_offset() const { return (part_ml_offset() + (size_t)records * 8 + 255) / 256 * 256; }
+  size_t bytes() const { return records ? counters_offset() + (size_t)counters * 8 : 0; }
 };
 
 // Measured prefill costs on one MI355X CU, for the planner's choice of split
@@ -90,6 +102,77 @@ constexpr double kPrefillItemUs = 4.5;
 constexpr double kMergeLaunchUs = 5.0;
 constexpr double kRecordBytesPerUs = 5.0e6;
 constexpr int kCusPerXcd = 32;
+
+// Decode merge choice.  The merge launch after a decode kernel costs an
+// empty kernel's time there (1.8-2.1 us measured on MI355X) plus the cold
+// round trip of its records (2-2.5 us).  The in-launch merge makes every
+// block wait, before it retires, for its record stores and one counter round
+// trip (kArrivalUs), which delays the blocks queued behind it once per wave of
+// resident blocks, and leaves the last split of each (row, kv head) a fold at
+// the tail (kInLaunchFoldUs).  Resident decode blocks: 256 CUs x 4 (the
+// kernels take 96-220 VGPRs per lane).
+constexpr double kDecodeMergeLaunchUs = 4.0;
+constexpr double kArrivalUs = 1.5;
+constexpr double kInLaunchFoldUs = 1.0;
+constexpr int64_t kDecodeResidentBlocks = 1024;
+// Decode kernel latency model: a launch floor, then whichever is longer of
+// streaming the KV bytes and the rounds of the items each resident block
+// runs one after another.
+constexpr double kDecodeFloorUs = 2.0;
+constexpr double kDecodeBytesPerUs = 5.5e6;
+constexpr double kDecodeRoundUs = 1.2;
+
+// Modelled time of a decode launch and its merge: `items` blocks of `rounds`
+// rounds over kv_bytes; split: some row has several splits, merged in the
+// launch (in_launch) or by the merge launch.
+double decode_launch_us(int64_t items, int rounds, double kv_bytes, bool split, bool in_launch) {
+  const double waves = (double)ceil_div(items, kDecodeResidentBlocks);
+  double us = kDecodeFloorUs + std::max(kv_bytes / kDecodeBytesPerUs, rounds * kDecodeRoundUs * waves);
+  if (split) us += in_launch ? kArrivalUs * waves + kInLaunchFoldUs : kDecodeMergeLaunchUs;
+  return us;
+}
+
+// The in-launch merge pays when its block waits and tail fold cost less
+// than the merge launch.
+bool decode_merge_in_launch_pays(int64_t items) {
+  return kArrivalUs * (double)ceil_div(items, kDecodeResidentBlocks) + kInLaunchFoldUs < kDecodeMergeLaunchUs;
+}
+
+// Rounds per decode item of rows [row0, row0 + nrows) (1 or
+// kDecodeItemRounds).  Launches with at least kDecodeManyItems one-round
+// items take kDecodeItemRounds: fewer, longer items cut the split records and
+// per-item work.  Smaller launches compare, by decode_launch_us, one-round
+// items against kDecodeItemRounds-round items when those bring every split
+// row within the in-launch merge (fusable: Hkv a multiple of 8 and no split
+// prefill row in the launch); longer items trade latency for the merge launch.
+// Measured on MI355X (cfg3 seeds 1 and 3, one round + merge launch against
+// four rounds + in-launch merge): 10.2 / 11.9 us and 13.6 / 12.8 us; the
+// model picks the faster of each.
+int choose_decode_rounds(const Geometry &g, const std::vector<int32_t> &counts, const std::vector<int32_t> &lengths,
+                         int64_t row0, int nrows, int G, int dp, int qr, bool fusable) {
+  int64_t items[2] = {0, 0}, max_splits[2] = {1, 1};
+  double kv_bytes = 0;
+  const int rounds[2] = {1, kDecodeItemRounds};
+  for (int r = 0; r < nrows; ++r) {
+    const int64_t qv = (int64_t)counts[row0 + r] * G, len = lengths[row0 + r];
+    if (qv <= 0 || qv > kDecodeMaxQueryVectors) continue;
+    kv_bytes += 4.0 * (double)(len * g.Hkv * g.D);
+    for (int o = 0; o < 2; ++o) {
+      const int64_t splits = ceil_div(len, rounds[o] * decode_tokens_per_item(dp, qr));
+      items[o] += g.Hkv * splits;
+      max_splits[o] = std::max(max_splits[o], splits);
+    }
+  }
+  if (items[0] >= kDecodeManyItems) return kDecodeItemRounds;
+  if (!fusable || max_splits[1] > kMergeSerialSplits) return 1;
+  double us[2];
+  for (int o = 0; o < 2; ++o) {
+    const bool split = max_splits[o] > 1;
+    const bool in_launch = max_splits[o] <= kMergeSerialSplits && decode_merge_in_launch_pays(items[o]);
+    us[o] = decode_launch_us(items[o], rounds[o], kv_bytes, split, in_launch);
+  }
+  return us[1] < us[0] ? kDecodeItemRounds : 1;
+}
 
 // 64-key tiles of prefill item (split, query tile) of row rs: the key range
 // of prefill.hip's split_range for that tile.
@@ -195,6 +278,56 @@ int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
   return best_keys;
 }
 
+// Whether a group's decode launch can merge its own split rows: it has split
+// decode rows and no split prefill row (whose records need the merge launch
+// anyway), every split row has at most kMergeSerialSplits splits (the merge
+// layout the in-launch fold reproduces), and Hkv is a multiple of 8 (the
+// kernel gives XCD x the kv heads h = x mod 8 of every row).
+bool decode_merge_fusable(const Group &grp, int64_t Hkv) {
+  if (grp.dec_items == 0 || grp.merge_items == 0 || Hkv % 8 != 0) return false;
+  if (grp.merge_max_splits > kMergeSerialSplits) return false;
+  for (int r = 0; r < grp.pre.nrows; ++r)
+    if (grp.pre.rows[r].nsplit > 1) return false;
+  return true;
+}
+
+// Whether this device deals consecutive blocks to its 8 XCDs in turn, probed
+// once per device on a stream that is not being captured.  Until the probe
+// has run (a first call made under capture), and if it disagrees, the merge
+// launch is used.
+bool xcd_dispatch_round_robin(hipStream_t stream) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex lock;
+  static int8_t known[kMaxDevices] = {};  // 0 unknown, 1 round robin, -1 not
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> guard(lock);
+  if (known[device] == 0) {
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return false;
+    bool round_robin = false;
+    if (probe_xcd_dispatch(&round_robin, stream) != hipSuccess) return false;
+    known[device] = round_robin ? 1 : -1;
+  }
+  return known[device] == 1;
+}
+
+// XINFER_DECODE_MERGE_LAUNCH=1 keeps every decode split on the merge launch
+// (read once per process): the check that both paths give the same bits.
+bool merge_launch_forced() {
+  static const bool forced = [] {
+    const char *value = std::getenv("XINFER_DECODE_MERGE_LAUNCH");
+    return value != nullptr && value[0] == '1';
+  }();
+  return forced;
+}
+
+// A nonzero tag below 2^36 for every decode launch with the in-launch merge.
+uint64_t next_launch_tag() {
+  static std::atomic<uint64_t> sequence{0};
+  return sequence.fetch_add(1, std::memory_order_relaxed) % ((uint64_t(1) << 36) - 1) + 1;
+}
+
 // counts/lengths: per-row real queries and populated KV lengths (validated).
 Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std::vector<int32_t> &lengths) {
   Plan plan;
@@ -215,17 +348,13 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
       if (qv > 0 && qv <= kDecodeMaxQueryVectors) max_qv = std::max(max_qv, qv);
     }
     grp.dec_qr = pow2_at_least(max_qv);
-    // kDecodeItemRounds rounds per decode item when one-round items would
-    // give at least kDecodeManyItems blocks: fewer, longer items cut the split
-    // records and per-item work; small batches keep one round for the
-    // parallelism.
-    int64_t one_round_items = 0;
+    bool prefill_split = false;
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t qv = (int64_t)counts[row0 + r] * G;
-      if (qv > 0 && qv <= kDecodeMaxQueryVectors)
-        one_round_items += g.Hkv * ceil_div(lengths[row0 + r], decode_tokens_per_item(dp, grp.dec_qr));
+      if (qv > kDecodeMaxQueryVectors && prefill_splits(lengths[row0 + r], split_keys) > 1) prefill_split = true;
     }
-    grp.dec_rounds = one_round_items >= kDecodeManyItems ? kDecodeItemRounds : 1;
+    grp.dec_rounds = choose_decode_rounds(g, counts, lengths, row0, grp.nrows, G, dp, grp.dec_qr,
+                                          g.Hkv % 8 == 0 && !prefill_split);
     const int tpi = grp.dec_rounds * decode_tokens_per_item(dp, grp.dec_qr);
     for (int r = 0; r < grp.nrows; ++r) {
       const int64_t b = row0 + r;
@@ -266,6 +395,8 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
       AttnArgs &a = decode ? grp.dec : grp.pre;
       a.rows[a.nrows++] = rs;
     }
+    grp.dec_fusable = decode_merge_fusable(grp, g.Hkv);
+    if (grp.dec_fusable) plan.counters = std::max<int64_t>(plan.counters, grp.dec_items);
     plan.groups.push_back(grp);
   }
   return plan;
@@ -298,6 +429,14 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
     }
     grp.dec.total_items = grp.dec_items;
     grp.pre.total_items = grp.pre_items;
+    grp.dec.arrive_ctr = nullptr;
+    grp.dec.tag = 0;
+    if (grp.dec_fusable && !merge_launch_forced() && decode_merge_in_launch_pays(grp.dec_items) &&
+        xcd_dispatch_round_robin(stream)) {
+      grp.dec.arrive_ctr = reinterpret_cast<uint64_t *>(static_cast<char *>(workspace) + plan.counters_offset());
+      grp.dec.tag = next_launch_tag();
+      grp.merge_items = 0;  // every split row is a decode row, merged in the launch
+    }
     if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_rounds, grp.dec_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
     if (grp.pre_items > 0) {

@@ -76,6 +76,7 @@ constexpr int kDecodeRounds = kDecodeItemRounds;
 
 struct DecodeItem {
   int b, h, split, nsplit, cnt, L, t0, t1;
+  int first;  // item of split 0 of this (row, kv head)
   int64_t rec_begin;
 };
 
@@ -88,6 +89,8 @@ struct DecodeParams {
   float *part_o, *part_ml;
   float scale_log2;
   int32_t D, G, T;
+  uint64_t *arrive_ctr;  // in-launch merge (merge_in_launch), else null
+  uint64_t tag;
 };
 
 __device__ __forceinline__ DecodeItem locate_item(const RowSched &rs, int item, int tok_item) {
@@ -101,6 +104,7 @@ __device__ __forceinline__ DecodeItem locate_item(const RowSched &rs, int item, 
   it.L = rs.length;
   it.t0 = it.split * tok_item;
   it.t1 = min(it.L, it.t0 + tok_item);
+  it.first = rs.item_begin + it.h * rs.nsplit;
   it.rec_begin = rs.rec_begin;
   return it;
 }
@@ -195,6 +199,106 @@ struct DecodeShared {
   float red_o[4][QR][DP];
   float red_m[4][QR], red_l[4][QR];
 };
+
+// In-launch merge of one (row, kv head)'s split records, called by every
+// thread of a block that has just written its records (AttnArgs::arrive_ctr
+// set).  The planner takes this path only for launches whose split rows have
+// at most kMergeSerialSplits splits and whose Hkv is a multiple of 8, and the
+// kernel then runs every split of a (row, kv head) on one XCD (block b on XCD
+// b % 8, which probe_xcd_dispatch checks once per device), so the records meet
+// in that XCD's L2.  Each block, once its record stores are acknowledged,
+// counts its arrival on the (row, kv head)'s counter; the last to arrive reads
+// the records past its CU's L1 and folds them as merge.hip's one-thread-per-
+// (vector, 4 features) layout does -- splits in increasing order, with the
+// products fused as that kernel compiles them (l = fma(l_old, a, ls w), o =
+// fma(os, w, o_old a)) -- so that both paths give the same bits, and resets
+// the counter to zero.
+//
+// Counter word: arrivals (bits 0-11), XCC of the first arrival (12-15),
+// arrivals from another XCC (16-27), the launch's tag (28-63).  The first
+// arrival claims a word that does not carry this launch's tag (zero after the
+// previous launch's reset, or whatever the workspace held) by compare-and-
+// swap; every other arrival adds itself with one fetch-and-add, so no arrival
+// waits behind another.  A (row, kv head) whose splits ran on more than one
+// XCC gets NaN outputs rather than a fold of records another L2 may hold.
+template <int DP>
+__device__ void merge_in_launch(const DecodeParams &a, const DecodeItem &it, int qrows) {
+  __shared__ uint32_t arrival;
+  const int tid = threadIdx.x;
+  __builtin_amdgcn_s_waitcnt(0);  // this thread's record stores are acknowledged
+  __syncthreads();
+  if (tid == 0) {
+    uint32_t xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    xcc &= 15u;
+    uint64_t *const ctr = a.arrive_ctr + it.first;
+    const uint64_t tag = a.tag;
+    uint64_t seen = 0;
+    bool claimed = false;
+    // Ends after at most two attempts: only this launch's first arrival
+    // writes its tag, and no reset happens before every arrival is counted.
+    while ((seen >> 28) != tag) {
+      if (__hip_atomic_compare_exchange_strong(ctr, &seen, (tag << 28) | ((uint64_t)xcc << 12) | 1u,
+                                               __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) {
+        claimed = true;
+        break;
+      }
+    }
+    uint32_t count = 1, mixed = 0;
+    if (!claimed) {
+      const bool other = ((seen >> 12) & 15u) != xcc;
+      const uint64_t before = __hip_atomic_fetch_add(ctr, (uint64_t)1 + (other ? (uint64_t)1 << 16 : 0),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      count = (uint32_t)(before & 0xfffu) + 1;
+      mixed = (uint32_t)((before >> 16) & 0xfffu) + (other ? 1u : 0u);
+    }
+    const bool last = count == (uint32_t)it.nsplit;
+    if (last) __hip_atomic_store(ctr, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    arrival = !last ? 0u : (mixed == 0 ? 1u : 2u);
+  }
+  __syncthreads();
+  const uint32_t flag = arrival;
+  if (flag == 0) return;
+
+  constexpr int FQ = DP / 4;  // feature quads of a padded vector
+  const int D = a.D, G = a.G, nsplit = it.nsplit;
+  // Record (split s, vector j) of this (row, kv head): rec0 + s * qrows + j.
+  const int64_t rec0 = it.rec_begin + (int64_t)it.h * nsplit * qrows;
+  const __amdgpu_buffer_rsrc_t o_rsrc = buffer_rsrc(a.part_o + rec0 * D, (uint32_t)(nsplit * qrows * D * 4));
+  const __amdgpu_buffer_rsrc_t ml_rsrc = buffer_rsrc(a.part_ml + 2 * rec0, (uint32_t)(nsplit * qrows * 8));
+  for (int idx = tid; idx < qrows * FQ; idx += blockDim.x) {
+    const int j = idx / FQ, f = idx - j * FQ;
+    if (f * 4 >= D) continue;
+    u32x2 ml[kMergeSerialSplits];
+    u32x4 o[kMergeSerialSplits];
+#pragma unroll
+    for (int s = 0; s < kMergeSerialSplits; ++s)
+      if (s < nsplit) {
+        ml[s] = buffer_load8_l2(ml_rsrc, (uint32_t)((s * qrows + j) * 8));
+        o[s] = buffer_load16_l2(o_rsrc, (uint32_t)(((s * qrows + j) * D + 4 * f) * 4));
+      }
+    float m = -INFINITY, l = 0.0f;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < kMergeSerialSplits; ++s) {
+      const float ms = __uint_as_float(ml[s].x);
+      if (s >= nsplit || ms == -INFINITY) continue;
+      const float ls = __uint_as_float(ml[s].y);
+      const f32x4 os = __builtin_bit_cast(f32x4, o[s]);
+      const float mn = fmaxf(m, ms);
+      const float wa = fast_exp2(m - mn), ws = fast_exp2(ms - mn);  // m = -inf -> wa = 0
+      l = __builtin_fmaf(l, wa, ls * ws);
+      acc = f32x4{__builtin_fmaf(os.x, ws, acc.x * wa), __builtin_fmaf(os.y, ws, acc.y * wa),
+                  __builtin_fmaf(os.z, ws, acc.z * wa), __builtin_fmaf(os.w, ws, acc.w * wa)};
+      m = mn;
+    }
+    const float inv = 1.0f / l;
+    uint16_t *dst = a.out + it.b * a.o_sb + (int64_t)(it.h * G + j % G) * a.o_sh + (int64_t)(j / G) * a.o_st + 4 * f;
+    *as_global(reinterpret_cast<u32x2 *>(dst)) =
+        flag == 1 ? u32x2{pack_bf16x2(acc.x * inv, acc.y * inv), pack_bf16x2(acc.z * inv, acc.w * inv)}
+                  : u32x2{0x7fc07fc0u, 0x7fc07fc0u};
+  }
+}
 
 // Compute one item from its registers (round 0 already issued); writes output
 // or partial records.
@@ -492,6 +596,7 @@ __device__ __forceinline__ void process_item(const DecodeParams &a, const Decode
         *as_global(reinterpret_cast<u32x2 *>(a.part_ml + 2 * rec)) = u32x2{__float_as_uint(mx), __float_as_uint(lsum)};
     }
   }
+  if (a.arrive_ctr != nullptr && it.nsplit > 1) merge_in_launch<DP>(a, it, qrows);
 }
 
 template <int DP, int QR, int ROUNDS>
@@ -504,13 +609,28 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   RowLookup<RowSched> rows;
   rows.load(a.rows);
   int nrows = a.nrows;
-  DecodeParams p{a.q, a.k, a.v, a.out, a.o_sb, a.o_sh, a.o_st, a.part_o, a.part_ml, a.scale_log2, a.D, a.G, a.T};
+  DecodeParams p{a.q,          a.k,  a.v,  a.out, a.o_sb, a.o_sh,       a.o_st, a.part_o, a.part_ml,
+                 a.scale_log2, a.D,  a.G,  a.T,   a.arrive_ctr, a.tag};
   asm volatile(""
                : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(nrows), XATTN_PIN_VIEW(p.q),
                  XATTN_PIN_VIEW(p.k), XATTN_PIN_VIEW(p.v), "+s"(p.out), "+s"(p.o_sb), "+s"(p.o_sh), "+s"(p.o_st),
                  "+s"(p.part_o), "+s"(p.part_ml), "+s"(p.scale_log2), "+s"(p.D), "+s"(p.G), "+s"(p.T));
-  const int item = blockIdx.x;
-  const DecodeItem it = locate_item(rows.find(a.rows, nrows, item), item, ROUNDS * S::TOK_ROUND);
+  DecodeItem it;
+  if (p.arrive_ctr == nullptr) {
+    const int item = blockIdx.x;
+    it = locate_item(rows.find(a.rows, nrows, item), item, ROUNDS * S::TOK_ROUND);
+  } else {
+    // In-launch merge (Hkv a multiple of 8): block b runs on XCD x = b % 8 and
+    // takes, row after row, the items of the kv heads h = x (mod 8), so every
+    // split of a (row, kv head) runs on one XCD and each XCD gets the same
+    // work.  XCD x's list holds Hkv / 8 heads of each row: row r's part of it
+    // starts at item_begin / 8.
+    const int x = (int)(blockIdx.x % 8), slot = (int)(blockIdx.x / 8);
+    const RowSched rs = rows.find(a.rows, nrows, 8 * slot);
+    const int local = slot - rs.item_begin / 8, hh = local / rs.nsplit;
+    const int h = 8 * hh + x, split = local - hh * rs.nsplit;
+    it = locate_item(rs, rs.item_begin + h * rs.nsplit + split, ROUNDS * S::TOK_ROUND);
+  }
   DecodeRegs<DP, QR> r;
   issue_item(p, it, r, wave, slot, dc);
   process_item<DP, QR, ROUNDS>(p, it, r, sh, wave, lane, slot, dc);
@@ -624,6 +744,31 @@ template <int DP>
 static hipError_t launch_decode_d(const AttnArgs &a, int qr, int rounds, int blocks, hipStream_t stream) {
   return rounds == kDecodeRounds ? launch_decode_r<DP, kDecodeRounds>(a, qr, blocks, stream)
                                  : launch_decode_r<DP, 1>(a, qr, blocks, stream);
+}
+
+// The XCC of each block of a small launch, for probe_xcd_dispatch.
+constexpr int kXccProbeBlocks = 64;
+__device__ uint32_t xcc_probe_ids[kXccProbeBlocks];
+
+__global__ void __launch_bounds__(64) xcc_probe_kernel() {
+  uint32_t xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (threadIdx.x == 0) xcc_probe_ids[blockIdx.x] = xcc & 15u;
+}
+
+hipError_t probe_xcd_dispatch(bool *round_robin, hipStream_t stream) {
+  hipLaunchKernelGGL(xcc_probe_kernel, dim3(kXccProbeBlocks), dim3(64), 0, stream);
+  hipError_t err = hipGetLastError();
+  uint32_t ids[kXccProbeBlocks] = {};
+  if (err == hipSuccess)
+    err = hipMemcpyFromSymbolAsync(ids, HIP_SYMBOL(xcc_probe_ids), sizeof(ids), 0, hipMemcpyDeviceToHost, stream);
+  if (err == hipSuccess) err = hipStreamSynchronize(stream);
+  if (err != hipSuccess) return err;
+  bool ok = true, distinct = false;
+  for (int b = 8; b < kXccProbeBlocks; ++b) ok = ok && ids[b] == ids[b % 8];
+  for (int b = 1; b < 8; ++b) distinct = distinct || ids[b] != ids[0];
+  *round_robin = ok && distinct;
+  return hipSuccess;
 }
 
 hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int blocks, hipStream_t stream) {

@@ -175,6 +175,15 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void *base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
 }
+// Loads with cache policy sc0 (scope beyond the CU): they miss in the CU's L1
+// and read the XCD's L2, i.e. data other CUs of the same XCD stored during
+// this launch.
+__device__ __forceinline__ u32x4 buffer_load16_l2(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, 0, 1));
+}
+__device__ __forceinline__ u32x2 buffer_load8_l2(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rsrc, voffset, 0, 1));
+}
 // Non-temporal (cache policy nt) 16-byte load, for data read exactly once.
 __device__ __forceinline__ u32x4 buffer_load16_stream(__amdgpu_buffer_rsrc_t rsrc, uint32_t voffset, uint32_t soffset) {
   return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rsrc, voffset, soffset, 2));

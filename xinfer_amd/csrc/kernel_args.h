@@ -42,6 +42,13 @@ struct AttnArgs {
   // runs item xcd_begin[b % 8] + b / 8 while below xcd_begin[b % 8 + 1]).
   // The planner cuts the item list into 8 runs of about equal work.
   int32_t xcd_begin[9];
+  // Decode in-launch merge (decode.hip: merge_in_launch); null: split records
+  // go to the merge launch.  One 64-bit arrival counter per decode item, the
+  // one of a (row, kv head)'s first item serving it; every counter is left at
+  // zero when the launch ends.  tag: nonzero, below 2^36, new for every
+  // launch the host makes.
+  uint64_t *arrive_ctr;
+  uint64_t tag;
 };
 
 // Merge of split partial records (merge.hip): one work item per query vector.

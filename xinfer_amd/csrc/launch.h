@@ -25,6 +25,15 @@ hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t s
 
 // Merges a.total_items query vectors; max_splits picks the thread layout.
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream);
+// Splits per query vector up to which the merge gives each (vector, 4
+// features) one thread that folds the splits in increasing order.  The decode
+// kernel's in-launch merge serves only such launches and folds the same way.
+constexpr int kMergeSerialSplits = 8;
+
+// Whether the device gives consecutive blocks of a launch to its 8 XCDs in
+// turn (block b on the XCD of block b % 8), which the decode kernel's
+// in-launch merge relies on: a small probe launch, synchronised on `stream`.
+hipError_t probe_xcd_dispatch(bool *round_robin, hipStream_t stream);
 
 // Graph-capture decode: the decode kernel over `blocks` blocks, then the merge
 // of every query vector of the capacity layout; max_splits = splits of a

@@ -29,6 +29,7 @@
 // reads in one L2.
 #include "device_common.h"
 #include "kernel_args.h"
+#include "launch.h"
 
 namespace xattn {
 
@@ -165,9 +166,6 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   fold_and_write<FS, SG>(red, part_o, part_ml, o_base, o_step, ml_base, ml_step, mr.nsplit, vvalid && d < D, sg, fl,
                          out + mr.batch * o_sb + (int64_t)(h * G + g) * o_sh + (int64_t)i * o_st + d);
 }
-
-// Splits at or below this count use one thread per (vector, 4 features).
-constexpr int kMergeSerialSplits = 8;
 
 // Feature lanes per block past kMergeSliceSplits splits: 64 features, 256
 // contiguous bytes of each record.  Measured on MI355X: slicing takes a
