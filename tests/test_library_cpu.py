@@ -284,6 +284,54 @@ def test_prefill_split_choice(lib):
     assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) > 3 * tiles * 128
 
 
+def decode_workspace(lib, counts, lengths, hq, hkv, d, capacity):
+    q, k = view([len(counts), hq, max(counts), d]), view([len(counts), hkv, capacity, d])
+    offsets = [0]
+    for count in counts:
+        offsets.append(offsets[-1] + count)
+    offsets.append(0)
+    for length in lengths:
+        offsets.append(offsets[-1] + length)
+    host = (ctypes.c_int32 * len(offsets))(*offsets)
+    return lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(q), ctypes.byref(k), host)
+
+
+def expected_workspace(records, d, counters):
+    """capi.cpp's layout: fp32 outputs, then (m, l) pairs, then the decode
+    launch's arrival counters, each region starting on a 256-byte boundary."""
+    align = lambda n: -(-n // 256) * 256
+    return align(align(records * d * 4) + records * 8) + counters * 8
+
+
+def test_decode_item_rounds_and_in_launch_merge_counters(lib):
+    """The planner's decode choices, read from the workspace it asks for.
+
+    Head dim 128, 16 query / 8 KV heads, one query per row: 2 query vectors
+    per KV head, 128 keys per one-round item, 512 per four-round item.  A
+    launch whose split rows all have at most 8 splits (and Hkv a multiple of
+    8) gets one arrival counter per decode item for the in-launch merge."""
+    # cfg1: one row of 1024 keys, one-round items, 8 splits: in-launch merge.
+    assert decode_workspace(lib, [1], [1024], 16, 8, 128, 4096) == expected_workspace(8 * 8 * 2, 128, 8 * 8)
+    # cfg3 seed 1's lengths: the 2170-key row has 17 one-round splits; four
+    # rounds would fit the in-launch merge, but the latency model keeps one
+    # round and the merge launch.
+    lengths = [24, 75, 81, 54, 755, 34, 390, 2170]
+    splits = [-(-length // 128) for length in lengths]
+    records = 8 * 2 * sum(s for s in splits if s > 1)
+    assert decode_workspace(lib, [1] * 8, lengths, 16, 8, 128, 16384) == expected_workspace(records, 128, 0)
+    # cfg3 seed 3's lengths: four-round items bring the longest row to 7
+    # splits, and the model takes them with the in-launch merge.
+    lengths = [20, 116, 3394, 53, 3006, 1084, 63, 322]
+    splits = [-(-length // 512) for length in lengths]
+    records = 8 * 2 * sum(s for s in splits if s > 1)
+    assert decode_workspace(lib, [1] * 8, lengths, 16, 8, 128, 16384) == expected_workspace(
+        records, 128, 8 * sum(splits))
+    # Four KV heads: no in-launch merge, whatever the splits.
+    assert decode_workspace(lib, [1], [1024], 16, 4, 128, 4096) == expected_workspace(4 * 8 * 4, 128, 0)
+    # Nine splits: past the in-launch merge's layout.
+    assert decode_workspace(lib, [1], [1100], 16, 8, 128, 4096) == expected_workspace(8 * 9 * 2, 128, 0)
+
+
 def test_operator_schemas_tags_and_fakes(library_path):
     from xinfer_amd.attention import attention_c_shims, cache_extent, load_attention_ops
 
