@@ -292,9 +292,12 @@ bool decode_merge_fusable(const Group &grp, int64_t Hkv) {
 }
 
 // Whether this device deals consecutive blocks to its 8 XCDs in turn, probed
-// once per device on a stream that is not being captured.  Until the probe
-// has run (a first call made under capture), and if it disagrees, the merge
-// launch is used.
+// once per device.  The probe runs on a private non-blocking stream, with
+// this thread in relaxed capture mode, so that neither the caller's stream
+// nor a capture another stream holds sees its launch, copy or synchronise.
+// A first call made while the caller's stream is being captured skips the
+// probe; until the probe has run, and if it disagrees, the merge launch is
+// used.
 bool xcd_dispatch_round_robin(hipStream_t stream) {
   constexpr int kMaxDevices = 64;
   static std::mutex lock;
@@ -305,8 +308,15 @@ bool xcd_dispatch_round_robin(hipStream_t stream) {
   if (known[device] == 0) {
     hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
     if (hipStreamIsCapturing(stream, &status) != hipSuccess || status != hipStreamCaptureStatusNone) return false;
+    hipStreamCaptureMode mode = hipStreamCaptureModeRelaxed;
+    if (hipThreadExchangeStreamCaptureMode(&mode) != hipSuccess) return false;
+    hipStream_t probe_stream = nullptr;
     bool round_robin = false;
-    if (probe_xcd_dispatch(&round_robin, stream) != hipSuccess) return false;
+    hipError_t err = hipStreamCreateWithFlags(&probe_stream, hipStreamNonBlocking);
+    if (err == hipSuccess) err = probe_xcd_dispatch(&round_robin, probe_stream);
+    if (probe_stream != nullptr) (void)hipStreamDestroy(probe_stream);
+    (void)hipThreadExchangeStreamCaptureMode(&mode);
+    if (err != hipSuccess) return false;
     known[device] = round_robin ? 1 : -1;
   }
   return known[device] == 1;
