@@ -241,7 +241,8 @@ int32_t prefill_splits(int64_t len, int64_t split_keys) {
 
 // Keys per prefill split for the call: among splits that give about 256,
 // 512, 1024 or 2048 items (at least kPrefillMinSplitKeys keys), the one whose
-// launch, simulated as dispatched, plus its merge launch, is fastest.  More,
+// launch, simulated as dispatched, plus its merge launch and the records'
+// two trips through HBM, is fastest.  More,
 // smaller items even out ragged rows; they cost per-item overhead, records
 // and merge traffic.
 int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
@@ -269,7 +270,8 @@ int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
       if (rs.nsplit > 1) records += g.Hkv * rs.nsplit * rs.ntiles * kPrefillTileQ;
     }
     double us = simulated_prefill_us(prefill_item_work(rows.data(), (int)rows.size(), g.Hkv, G, dp));
-    if (records) us += kMergeLaunchUs + (double)records * (dp * 4 + 8) / kRecordBytesPerUs;
+    // Records cross HBM twice: written by the prefill kernel, read by the merge.
+    if (records) us += kMergeLaunchUs + 2.0 * (double)records * (dp * 4 + 8) / kRecordBytesPerUs;
     if (target == 256 || us < best_us) {
       best_us = us;
       best_keys = split_keys;
