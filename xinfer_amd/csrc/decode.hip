@@ -281,8 +281,9 @@ __device__ void merge_in_launch(const DecodeParams &a, const DecodeItem &it, int
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int s = 0; s < kMergeSerialSplits; ++s) {
+      if (s >= nsplit) break;
       const float ms = __uint_as_float(ml[s].x);
-      if (s >= nsplit || ms == -INFINITY) continue;
+      if (ms == -INFINITY) continue;
       const float ls = __uint_as_float(ml[s].y);
       const f32x4 os = __builtin_bit_cast(f32x4, o[s]);
       const float mn = fmaxf(m, ms);
