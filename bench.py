@@ -334,8 +334,10 @@ def cpu_baseline(w, inputs, budget_s):
 
     Legs (median of repeated runs, each leg bounded by ``budget_s`` seconds):
 
-    * ``sdpa_bf16``: the reference's CPU path: per row
-      an index_copy_ of the new K/V into a CPU cache of the same capacity, then
+    * ``sdpa_bf16``: the reference's attention math on the host, as its own
+      tests state it (compiler/common/tests/test_attention.py:100-105: SDPA
+      with enable_gqa over each row's populated prefix): per row an
+      index_copy_ of the new K/V into a CPU cache of the same capacity, then
       torch SDPA on bf16 tensors with the explicit lower-right mask and
       enable_gqa, with all of torch's threads;
     * ``sdpa_bf16_1thread``: the same with one thread (the reference runtime

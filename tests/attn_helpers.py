@@ -53,7 +53,7 @@ def reference_attention(q, k, v, counts, lengths, scale):
 
 
 def assert_close_rows(actual, expected, counts, *, relative_l2=0.01, peak_relative=0.05):
-    """Reference test bounds per row (test_attention.py:112-113) plus the BASELINE gates."""
+    """Reference test bounds per row (test_attention.py:112-113) plus max-abs <= 2e-2 and mean-abs <= 2e-3."""
     for r, count in enumerate(counts):
         if not count:
             continue

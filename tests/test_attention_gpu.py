@@ -5,7 +5,7 @@ compiler/qwen35/tests/test_attention.py:244-297.  The reference's bitwise
 comparisons against ATen's own flash kernel pin ATen's rounding rather than the
 operator contract; they are replaced by the fp32 reference bounds the reference
 uses everywhere else (relative L2 < 0.01, peak relative <= 0.05) plus the
-BASELINE gates (max-abs <= 2e-2, mean-abs <= 2e-3).  Determinism, isolation
+tolerance gates of the benchmark definition (max-abs <= 2e-2, mean-abs <= 2e-3).  Determinism, isolation
 from other rows and from unused cache slots, zeroed padding, read-only inputs
 and the fake contract are checked bit for bit as in the reference.
 """
