@@ -282,6 +282,29 @@ def test_prefill_split_choice(lib):
     lengths = [14244, 13896, 2059, 4214, 12262, 14086, 12837, 9315]
     tiles = sum(4 * -(-count * 4 // 128) for count in counts)
     assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) > 3 * tiles * 128
+    # The split the dispatch model picks among every row's split-count change
+    # points: 3200-key splits (5, 5, 1, 2, 4, 5, 5, 3 splits per row; 241 split
+    # tiles per kv head), measured faster than the 2752-key splits of octave
+    # steps and than 3264-key splits (one split fewer on the 12837-key row).
+    assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) == 4 * 241 * 128
+
+
+def test_plans_are_recomputed_when_the_call_changes(lib):
+    """The per-thread cache of the last plan: alternating calls, each asking
+    for its workspace twice, get the workspace of a fresh plan every time."""
+    counts = [356, 138, 422, 459, 325, 298, 113, 124]
+    lengths = [14244, 13896, 2059, 4214, 12262, 14086, 12837, 9315]
+    ragged = prefill_records(lib, counts, lengths, 16, 4, 256, 16384)
+    uniform = prefill_records(lib, [512], [2048], 16, 8, 128, 4096)
+    for _ in range(2):
+        assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) == ragged
+        assert prefill_records(lib, counts, lengths, 16, 4, 256, 16384) == ragged
+        assert prefill_records(lib, [512], [2048], 16, 8, 128, 4096) == uniform
+        # Same counts and lengths, other geometry: its own plan.
+        assert prefill_records(lib, [512], [2048], 16, 8, 64, 4096) == uniform
+        assert prefill_records(lib, [512], [2048], 16, 8, 128, 4096) == uniform
+        shorter = [length - 1000 for length in lengths]
+        assert prefill_records(lib, counts, shorter, 16, 4, 256, 16384) != ragged
 
 
 def decode_workspace(lib, counts, lengths, hq, hkv, d, capacity):

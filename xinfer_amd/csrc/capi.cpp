@@ -15,6 +15,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
+#include <functional>
 #include <mutex>
 #include <vector>
 
@@ -219,17 +220,20 @@ void xcd_runs(const std::vector<double> &work, int32_t *begin) {
 
 // Time of the prefill launch when the items run as the hardware dispatches
 // them: the blocks of each XCD, in order, to whichever of its CUs is free.
+// The CUs' finishing times are kept in a min-heap (which of several tied CUs
+// takes an item does not change the times that follow).
 double simulated_prefill_us(const std::vector<double> &work) {
   int32_t begin[9];
   xcd_runs(work, begin);
   double span = 0;
   for (int x = 0; x < 8; ++x) {
-    std::vector<double> free_at(kCusPerXcd, 0.0);
+    double free_at[kCusPerXcd] = {};  // all equal: already a heap
     for (int32_t i = begin[x]; i < begin[x + 1]; ++i) {
-      auto cu = std::min_element(free_at.begin(), free_at.end());
-      *cu += work[(size_t)i];
+      std::pop_heap(free_at, free_at + kCusPerXcd, std::greater<double>());
+      free_at[kCusPerXcd - 1] += work[(size_t)i];
+      std::push_heap(free_at, free_at + kCusPerXcd, std::greater<double>());
     }
-    span = std::max(span, *std::max_element(free_at.begin(), free_at.end()));
+    span = std::max(span, *std::max_element(free_at, free_at + kCusPerXcd));
   }
   return span;
 }
@@ -239,12 +243,19 @@ int32_t prefill_splits(int64_t len, int64_t split_keys) {
   return (int32_t)std::max<int64_t>(1, ceil_div(len, split_keys));
 }
 
-// Keys per prefill split for the call: among splits that give about 256,
-// 512, 1024 or 2048 items (at least kPrefillMinSplitKeys keys), the one whose
-// launch, simulated as dispatched, plus its merge launch and the records'
-// two trips through HBM, is fastest.  More,
-// smaller items even out ragged rows; they cost per-item overhead, records
-// and merge traffic.
+// Keys per prefill split for the call: the split size, from about 256 to
+// 2048 items' worth (at least kPrefillMinSplitKeys keys), whose launch,
+// simulated as dispatched, plus its merge launch and the records' two trips
+// through HBM, is fastest.  More, smaller items even out ragged rows; they
+// cost per-item overhead, records and merge traffic.  The simulated span
+// moves in jumps, when some row's split count changes, so the candidates are
+// those change points: for each row and split count n, the smallest multiple
+// of 64 keys that cuts the row into n splits (on the ragged D = 256 batch of
+// 2235 tokens, cfg5, 3200-key splits measured 10 us faster than 2752-key
+// ones, and 3264-key splits, one split fewer on one row, 4 us slower than
+// 3200).  Candidates are simulated in increasing order of a lower bound on
+// their time (total work over 256 CUs, or the longest item, plus the
+// records), until that bound passes the best time found.
 int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
                           const std::vector<int32_t> &lengths, int G, int dp) {
   int64_t prefill_keys = 0;
@@ -259,22 +270,84 @@ int64_t choose_split_keys(const Geometry &g, const std::vector<int32_t> &counts,
     rs.ntiles = (int32_t)ceil_div(qv, kPrefillTileQ);
     rows.push_back(rs);
   }
-  int64_t best_keys = kPrefillMinSplitKeys;
-  double best_us = 0;
-  for (int64_t target = 256; target <= 2048; target *= 2) {
-    const int64_t split_keys =
-        std::max(kPrefillMinSplitKeys, ceil_div(ceil_div(prefill_keys, target), 64) * 64);
-    int64_t records = 0;
-    for (RowSched &rs : rows) {
-      rs.nsplit = prefill_splits(rs.length, split_keys);
-      if (rs.nsplit > 1) records += g.Hkv * rs.nsplit * rs.ntiles * kPrefillTileQ;
+  if (rows.empty()) return kPrefillMinSplitKeys;
+  auto keys_for = [&](int64_t target) {
+    return std::max(kPrefillMinSplitKeys, ceil_div(ceil_div(prefill_keys, target), 64) * 64);
+  };
+  const int64_t lo = keys_for(2048), hi = keys_for(256);
+  std::vector<int64_t> keys = {lo, hi};
+  for (const RowSched &rs : rows)
+    for (int64_t n = ceil_div(rs.length, hi); n <= ceil_div(rs.length, lo); ++n) {
+      const int64_t k = std::max(kPrefillMinSplitKeys, ceil_div(ceil_div(rs.length, n), 64) * 64);
+      if (k >= lo && k <= hi) keys.push_back(k);
     }
-    double us = simulated_prefill_us(prefill_item_work(rows.data(), (int)rows.size(), g.Hkv, G, dp));
+  std::sort(keys.begin(), keys.end());
+  keys.erase(std::unique(keys.begin(), keys.end()), keys.end());
+  // Per row and split count: the work of one kv head's items and its longest
+  // item (every kv head has the same items).
+  struct RowWork {
+    int32_t nsplit;
+    double total, longest;
+    std::vector<double> items;  // one kv head's items, in order (split, tile)
+  };
+  std::vector<std::vector<RowWork>> row_work(rows.size());
+  auto work_of = [&](size_t r, int32_t nsplit) -> const RowWork & {
+    for (const RowWork &w : row_work[r])
+      if (w.nsplit == nsplit) return w;
+    RowSched rs = rows[r];
+    rs.nsplit = nsplit;
+    RowWork w{nsplit, 0.0, 0.0, {}};
+    w.items.reserve((size_t)nsplit * rs.ntiles);
+    for (int split = 0; split < nsplit; ++split)
+      for (int tile = 0; tile < rs.ntiles; ++tile) {
+        const double us = prefill_item_tiles(rs, G, split, tile) * prefill_tile_us(dp) + kPrefillItemUs;
+        w.total += us;
+        w.longest = std::max(w.longest, us);
+        w.items.push_back(us);
+      }
+    row_work[r].push_back(w);
+    return row_work[r].back();
+  };
+  struct Candidate {
+    double bound, records_us;
+    int64_t split_keys;
+  };
+  std::vector<Candidate> cands;
+  cands.reserve(keys.size());
+  for (const int64_t split_keys : keys) {
+    int64_t records = 0;
+    double total = 0, longest = 0;
+    for (size_t r = 0; r < rows.size(); ++r) {
+      const int32_t nsplit = prefill_splits(rows[r].length, split_keys);
+      if (nsplit > 1) records += g.Hkv * nsplit * rows[r].ntiles * kPrefillTileQ;
+      const RowWork &w = work_of(r, nsplit);
+      total += g.Hkv * w.total;
+      longest = std::max(longest, w.longest);
+    }
     // Records cross HBM twice: written by the prefill kernel, read by the merge.
-    if (records) us += kMergeLaunchUs + 2.0 * (double)records * (dp * 4 + 8) / kRecordBytesPerUs;
-    if (target == 256 || us < best_us) {
+    const double records_us =
+        records ? kMergeLaunchUs + 2.0 * (double)records * (dp * 4 + 8) / kRecordBytesPerUs : 0.0;
+    cands.push_back({std::max(total / (8.0 * kCusPerXcd), longest) + records_us, records_us, split_keys});
+  }
+  // Ties go to the larger split (fewer items and records).
+  std::sort(cands.begin(), cands.end(), [](const Candidate &a, const Candidate &b) {
+    return a.bound != b.bound ? a.bound < b.bound : a.split_keys > b.split_keys;
+  });
+  int64_t best_keys = cands.front().split_keys;
+  double best_us = -1;
+  std::vector<double> work;
+  for (const Candidate &c : cands) {
+    if (best_us >= 0 && c.bound >= best_us) break;
+    // Items in launch order (row, kv head, split, tile), as prefill_item_work lists them.
+    work.clear();
+    for (size_t r = 0; r < rows.size(); ++r) {
+      const RowWork &w = work_of(r, prefill_splits(rows[r].length, c.split_keys));
+      for (int64_t h = 0; h < g.Hkv; ++h) work.insert(work.end(), w.items.begin(), w.items.end());
+    }
+    const double us = simulated_prefill_us(work) + c.records_us;
+    if (best_us < 0 || us < best_us || (us == best_us && c.split_keys > best_keys)) {
       best_us = us;
-      best_keys = split_keys;
+      best_keys = c.split_keys;
     }
   }
   return best_keys;
@@ -412,6 +485,35 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
     plan.groups.push_back(grp);
   }
   return plan;
+}
+
+// The plan of this thread's last call.  A model step calls the operator once
+// per layer with the same counts and lengths, and every call plans twice (its
+// workspace size, then the launch), while planning a ragged prefill batch
+// simulates its dispatch at several split sizes (about 0.36 ms for the
+// batch-8 D = 256 prefill of 2235 tokens); a call whose geometry, counts and
+// lengths equal the last one's reuses that plan.  A plan depends on nothing
+// else: not on the device, the stream or the tensors' addresses.
+Plan cached_plan(const Geometry &g, const std::vector<int32_t> &counts, const std::vector<int32_t> &lengths) {
+  struct Entry {
+    bool valid = false;
+    Geometry g{};
+    std::vector<int32_t> counts, lengths;
+    Plan plan;
+  };
+  thread_local Entry last;
+  const bool same = last.valid && last.g.B == g.B && last.g.Hq == g.Hq && last.g.Hkv == g.Hkv &&
+                    last.g.T == g.T && last.g.D == g.D && last.g.C == g.C && last.counts == counts &&
+                    last.lengths == lengths;
+  if (!same) {
+    last.valid = false;
+    last.plan = make_plan(g, counts, lengths);
+    last.g = g;
+    last.counts = counts;
+    last.lengths = lengths;
+    last.valid = true;
+  }
+  return last.plan;
 }
 
 int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const xinfer_view4 &k,
@@ -636,7 +738,7 @@ size_t xinfer_batched_flash_attention_workspace_size(const xinfer_view4 *q, cons
   Geometry g;
   std::vector<int32_t> counts, lengths;
   if (check_batched(q, k, k, host_offsets, g, counts, lengths) != XINFER_OK) return 0;
-  return make_plan(g, counts, lengths).bytes();
+  return cached_plan(g, counts, lengths).bytes();
 }
 
 int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
@@ -649,7 +751,7 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
-  const Plan plan = make_plan(g, counts, lengths);
+  const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
   return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
@@ -713,7 +815,7 @@ int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_v
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
-  const Plan plan = make_plan(g, counts, lengths);
+  const Plan plan = cached_plan(g, counts, lengths);
   if (plan.bytes() > kScratchBytes) return XINFER_ERR_SCRATCH;
   // The device address of the static scratch on the current device (never
   // the host-side name of the array).
@@ -732,7 +834,7 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (int rc = check_output(g, out)) return rc;
-  const Plan plan = make_plan(g, counts, lengths);
+  const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
   return run_plan(plan, g, *q, *k, *v, scale, *out, workspace, static_cast<hipStream_t>(stream));
@@ -743,7 +845,7 @@ size_t xinfer_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer
   Geometry g;
   if (check_flash(q, k, k, valid_length, g) != XINFER_OK) return 0;
   std::vector<int32_t> counts(g.B, (int32_t)g.T), lengths(g.B, (int32_t)valid_length);
-  return make_plan(g, counts, lengths).bytes();
+  return cached_plan(g, counts, lengths).bytes();
 }
 
 int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
@@ -754,7 +856,7 @@ int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const x
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
   std::vector<int32_t> counts(g.B, (int32_t)g.T), lengths(g.B, (int32_t)valid_length);
-  const Plan plan = make_plan(g, counts, lengths);
+  const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
   return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
