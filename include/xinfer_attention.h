@@ -40,7 +40,7 @@ enum {
   XINFER_ERR_LAYOUT = 11,         /* feature stride != 1 or rows not 16-byte aligned */
   XINFER_ERR_CACHE = 12,          /* cache tensors not contiguous [B,H,C,D] / shape mismatch */
   XINFER_ERR_LAUNCH = 13,         /* a HIP kernel launch failed */
-  XINFER_ERR_ARGUMENT = 14,       /* null pointer or negative size */
+  XINFER_ERR_ARGUMENT = 14,       /* null pointer, negative size or stride, misaligned page table */
   XINFER_ERR_ROPE_SHAPE = 15,     /* xinfer_qk_norm_rope_append shapes (no reference message) */
   XINFER_ERR_EPS = 16,            /* RMSNorm epsilon not finite and >= 0 (no reference message) */
   XINFER_ERR_SCRATCH = 17,        /* the call needs more than XINFER_NOALLOC_SCRATCH_BYTES of scratch */
@@ -83,11 +83,21 @@ int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const x
  * `offsets` tensor of batched_attention_metadata (attention.py:27-40).  Row r
  * attends with its first count_r queries over k/v[r, :, :L_r], lower-right
  * causal; out[r, :, count_r:] is written as zeros.
+ *
+ * blocks: NULL, or the DEVICE int32 page table of attention.cpp:39-40, 56-58,
+ * 68-70, one entry per row at blocks[r * blocks_stride] (blocks_stride >= 0,
+ * the table's row stride; 4-byte aligned): row r then reads its keys and
+ * values from k/v[blocks[r]] instead of k/v[r], each entry clamped into
+ * [0, B).  The reference applies its table only when the cache capacity C is
+ * a multiple of 256; xinfer::batched_flash_attention passes it under that
+ * condition and NULL otherwise.  The kernels read it on the device: the
+ * identity table costs one scalar read per work item.
  * ------------------------------------------------------------------------- */
 size_t xinfer_batched_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
                                                      const int32_t *host_offsets);
 int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
-                                   const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                   const xinfer_view4 *v, const int32_t *host_offsets,
+                                   const int32_t *blocks, int64_t blocks_stride, double scale,
                                    void *out, void *workspace, size_t workspace_bytes, void *stream);
 
 /* Same operation with the output written through a caller-supplied view of
@@ -99,6 +109,7 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
  * spares compiler/qwen3/adapters/attention.py:61 its transpose copy. */
 int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4 *k,
                                        const xinfer_view4 *v, const int32_t *host_offsets,
+                                       const int32_t *blocks, int64_t blocks_stride,
                                        double scale, const xinfer_view4 *out, void *workspace,
                                        size_t workspace_bytes, void *stream);
 
@@ -110,7 +121,8 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
  * the cumulative offsets (int32 [2][B+1], batched_attention_metadata's
  * cuda_offsets); the kernels read every row's count and length from it when
  * they run, so nothing about the launch depends on host lengths and a
- * captured call stays valid after the caller rewrites device_offsets in place.
+ * captured call stays valid after the caller rewrites device_offsets in place
+ * (and the page table, read the same way).
  * The workspace size depends on the shapes only (all rows at capacity C).
  * Rows must take the decode path: T * (Hq/Hkv) <= 8, and B <= 64
  * (XINFER_ERR_CAPTURE_ROWS otherwise).  Device lengths are not validated on
@@ -120,7 +132,8 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
  * kernels are the same, but every launch covers the capacity. */
 size_t xinfer_batched_flash_attention_graph_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k);
 int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
-                                         const int32_t *device_offsets, double scale, void *out, void *workspace,
+                                         const int32_t *device_offsets, const int32_t *blocks,
+                                         int64_t blocks_stride, double scale, void *out, void *workspace,
                                          size_t workspace_bytes, void *stream);
 
 /* Allocation-free variant of xinfer_batched_flash_attention.  No counterpart in
@@ -138,6 +151,7 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
 #define XINFER_NOALLOC_SCRATCH_BYTES (32u << 20)
 int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_view4 *k,
                                            const xinfer_view4 *v, const int32_t *host_offsets,
+                                           const int32_t *blocks, int64_t blocks_stride,
                                            double scale, void *out, void *stream);
 
 /* ---------------------------------------------------------------------------

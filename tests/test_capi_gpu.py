@@ -57,12 +57,14 @@ def test_batched_through_c_abi(capi, gpu_ops):
     workspace = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
     out = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
     status = capi.xinfer_batched_flash_attention(
-        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, ctypes.c_double(dim**-0.5),
-        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size), stream())
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, None, ctypes.c_int64(0),
+        ctypes.c_double(dim**-0.5), ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()),
+        ctypes.c_size_t(size), stream())
     assert status == 0, capi.xinfer_status_string(status)
     if size:
         too_small = capi.xinfer_batched_flash_attention(
-            ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, ctypes.c_double(dim**-0.5),
+            ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, None, ctypes.c_int64(0),
+            ctypes.c_double(dim**-0.5),
             ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size - 1),
             stream())
         assert capi.xinfer_status_string(too_small).decode().startswith("Attention workspace")
@@ -141,7 +143,7 @@ def test_split_merge_survives_garbage_and_reused_workspace(capi, gpu_ops):
             workspace = torch.randint(0, 256, (size,), dtype=torch.uint8, device="cuda")
         out = torch.empty_like(q)
         status = capi.xinfer_batched_flash_attention(
-            ctypes.byref(view(q)), ctypes.byref(view(k)), ctypes.byref(view(v)), host_ptr,
+            ctypes.byref(view(q)), ctypes.byref(view(k)), ctypes.byref(view(v)), host_ptr, None, ctypes.c_int64(0),
             ctypes.c_double(dim**-0.5), ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()),
             ctypes.c_size_t(size), stream())
         assert status == 0, capi.xinfer_status_string(status)

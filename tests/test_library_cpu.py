@@ -107,11 +107,14 @@ def test_flash_validation_order_and_codes(lib):
     assert flash(lib, strided, k, 5) == 11
 
 
-def batched(lib, q, k, offsets, scale=0.1):
+ARGUMENT = 14  # XINFER_ERR_ARGUMENT
+
+
+def batched(lib, q, k, offsets, scale=0.1, blocks=None, stride=0):
     host = (ctypes.c_int32 * len(offsets))(*offsets)
     return lib.xinfer_batched_flash_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), host,
-                                              ctypes.c_double(scale), ctypes.c_void_p(1 << 20), None,
-                                              ctypes.c_size_t(0), None)
+                                              blocks, ctypes.c_int64(stride), ctypes.c_double(scale),
+                                              ctypes.c_void_p(1 << 20), None, ctypes.c_size_t(0), None)
 
 
 def test_batched_validation_codes(lib):
@@ -123,6 +126,9 @@ def test_batched_validation_codes(lib):
     assert batched(lib, q, k, [0, 3, 4, 0, 2, 9]) == 9   # length < count
     assert batched(lib, q, k, [0, 1, 2, 0, 65, 70]) == 9  # length > capacity
     assert batched(lib, q, k, [0, 1, 2, 0, 5, 9], scale=0.0) == 7
+    # A page table is a 4-byte aligned device pointer with a non-negative row stride.
+    assert batched(lib, q, k, [0, 1, 2, 0, 5, 9], blocks=ctypes.c_void_p((1 << 21) + 2), stride=1) == ARGUMENT
+    assert batched(lib, q, k, [0, 1, 2, 0, 5, 9], blocks=ctypes.c_void_p(1 << 21), stride=-1) == ARGUMENT
 
 
 def norm_rope(lib, q, k, rope, cache, eps=1e-6, cu_query=1 << 21):
@@ -158,7 +164,8 @@ def test_output_view_validation_codes(lib):
 
     def call(out):
         return lib.xinfer_batched_flash_attention_out(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), host,
-                                                      ctypes.c_double(0.1), out, None, ctypes.c_size_t(0), None)
+                                                      None, ctypes.c_int64(0), ctypes.c_double(0.1), out, None,
+                                                      ctypes.c_size_t(0), None)
 
     assert call(None) == 14
     assert call(ctypes.byref(view([2, 16, 5, 128]))) == 1
@@ -211,7 +218,7 @@ def test_noalloc_rejects_plans_beyond_its_scratch_before_any_launch(lib):
 
     def noalloc(qv, kv, offsets_, scale=1.0):
         return lib.xinfer_batched_flash_attention_noalloc(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),
-                                                          offsets_, ctypes.c_double(scale),
+                                                          offsets_, None, ctypes.c_int64(0), ctypes.c_double(scale),
                                                           ctypes.c_void_p(1 << 20), None)
 
     assert noalloc(q, k, host) == 17
@@ -245,8 +252,9 @@ def test_graph_mode_shapes_and_workspace(lib):
 
     def graph(qv, kv):
         return lib.xinfer_batched_flash_attention_graph(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),
-                                                        ctypes.c_void_p(1 << 21), ctypes.c_double(0.1),
-                                                        ctypes.c_void_p(1 << 20), None, ctypes.c_size_t(0), None)
+                                                        ctypes.c_void_p(1 << 21), None, ctypes.c_int64(0),
+                                                        ctypes.c_double(0.1), ctypes.c_void_p(1 << 20), None,
+                                                        ctypes.c_size_t(0), None)
 
     assert graph(view([1, 16, 5, 128]), view([1, 8, 256, 128])) == 18   # 10 query vectors per KV head
     assert graph(view([65, 16, 1, 128]), view([65, 8, 256, 128])) == 18

@@ -79,13 +79,14 @@ def run_both(capi, q, k, v, counts, lengths, scale):
     assert 0 < size <= SCRATCH_BYTES
     out = torch.full(q.shape, float("nan"), dtype=torch.bfloat16, device="cuda")
     status = capi.xinfer_batched_flash_attention_noalloc(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host,
-                                                         ctypes.c_double(scale), ctypes.c_void_p(out.data_ptr()),
-                                                         stream)
+                                                         None, ctypes.c_int64(0), ctypes.c_double(scale),
+                                                         ctypes.c_void_p(out.data_ptr()), stream)
     assert status == 0, capi.xinfer_status_string(status)
     workspace = torch.empty(size, dtype=torch.uint8, device="cuda")
     expected = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
     status = capi.xinfer_batched_flash_attention(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host,
-                                                 ctypes.c_double(scale), ctypes.c_void_p(expected.data_ptr()),
+                                                 None, ctypes.c_int64(0), ctypes.c_double(scale),
+                                                 ctypes.c_void_p(expected.data_ptr()),
                                                  ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size), stream)
     assert status == 0, capi.xinfer_status_string(status)
     torch.cuda.synchronize()
@@ -142,8 +143,9 @@ def test_noalloc_refuses_plans_beyond_its_scratch(capi):
     out = torch.full(q.shape, 7.0, dtype=torch.bfloat16, device="cuda")
     qv, kv = view(q), view(k)
     status = capi.xinfer_batched_flash_attention_noalloc(
-        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv), host_offsets(counts, lengths), ctypes.c_double(1 / 16),
-        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv), host_offsets(counts, lengths), None, ctypes.c_int64(0),
+        ctypes.c_double(1 / 16), ctypes.c_void_p(out.data_ptr()),
+        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
     assert status == 17, capi.xinfer_status_string(status)
     torch.cuda.synchronize()
     assert bool((out == 7.0).all())  # nothing was launched
@@ -174,8 +176,8 @@ with torch.cuda.stream(side):
     # kernels' first launches) before any capture.
     workspace = torch.empty(size, dtype=torch.uint8, device="cuda")
     expected = torch.empty(q.shape, dtype=torch.bfloat16, device="cuda")
-    status = lib.xinfer_batched_flash_attention(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, scale,
-                                                ctypes.c_void_p(expected.data_ptr()),
+    status = lib.xinfer_batched_flash_attention(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, None,
+                                                ctypes.c_int64(0), scale, ctypes.c_void_p(expected.data_ptr()),
                                                 ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size),
                                                 ctypes.c_void_p(side.cuda_stream))
     assert status == 0, lib.xinfer_status_string(status)
@@ -185,8 +187,8 @@ torch.cuda.synchronize()
 graph = torch.cuda.CUDAGraph()
 with torch.cuda.graph(graph):
     status = lib.xinfer_batched_flash_attention_noalloc(
-        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, scale, ctypes.c_void_p(out.data_ptr()),
-        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host, None, ctypes.c_int64(0), scale,
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
 assert status == 0, lib.xinfer_status_string(status)
 torch.cuda.synchronize()
 for replay in range(3):

@@ -482,6 +482,7 @@ Plan make_plan(const Geometry &g, const std::vector<int32_t> &counts, const std:
     }
     grp.dec_fusable = decode_merge_fusable(grp, g.Hkv);
     if (grp.dec_fusable) plan.counters = std::max<int64_t>(plan.counters, grp.dec_items);
+    if (grp.pre_items > 0) xcd_runs(prefill_item_work(grp.pre.rows, grp.pre.nrows, g.Hkv, G, dp), grp.pre.xcd_begin);
     plan.groups.push_back(grp);
   }
   return plan;
@@ -516,8 +517,16 @@ Plan cached_plan(const Geometry &g, const std::vector<int32_t> &counts, const st
   return last.plan;
 }
 
+// A page table (nullable) is a device int32 pointer with a non-negative row stride.
+int check_blocks(const int32_t *blocks, int64_t blocks_stride) {
+  if (blocks == nullptr) return XINFER_OK;
+  if ((reinterpret_cast<uintptr_t>(blocks) & 3u) != 0 || blocks_stride < 0) return XINFER_ERR_ARGUMENT;
+  return XINFER_OK;
+}
+
 int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const xinfer_view4 &k,
-             const xinfer_view4 &v, double scale, const xinfer_view4 &out, void *workspace, hipStream_t stream) {
+             const xinfer_view4 &v, const int32_t *blocks, int64_t blocks_stride, double scale,
+             const xinfer_view4 &out, void *workspace, hipStream_t stream) {
   const int G = (int)(g.Hq / g.Hkv);
   const int dp = padded_dim(g.D);
   float *part_o = static_cast<float *>(workspace);
@@ -540,6 +549,9 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
       a->G = G;
       a->Hkv = (int32_t)g.Hkv;
       a->T = (int32_t)g.T;
+      a->blocks = blocks;
+      a->blocks_stride = blocks_stride;
+      a->kv_rows = (int32_t)g.B;
     }
     grp.dec.total_items = grp.dec_items;
     grp.pre.total_items = grp.pre_items;
@@ -553,10 +565,7 @@ int run_plan(const Plan &plan, const Geometry &g, const xinfer_view4 &q, const x
     }
     if (grp.dec_items > 0 && launch_decode(grp.dec, dp, grp.dec_qr, grp.dec_rounds, grp.dec_items, stream) != hipSuccess)
       return XINFER_ERR_LAUNCH;
-    if (grp.pre_items > 0) {
-      xcd_runs(prefill_item_work(grp.pre.rows, grp.pre.nrows, g.Hkv, G, dp), grp.pre.xcd_begin);
-      if (launch_prefill(grp.pre, dp, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
-    }
+    if (grp.pre_items > 0 && launch_prefill(grp.pre, dp, stream) != hipSuccess) return XINFER_ERR_LAUNCH;
     if (grp.merge_items > 0) {
       MergeArgs &m = grp.merge;
       m.out = static_cast<uint16_t *>(const_cast<void *>(out.data));
@@ -742,19 +751,21 @@ size_t xinfer_batched_flash_attention_workspace_size(const xinfer_view4 *q, cons
 }
 
 int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
-                                   const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                   const xinfer_view4 *v, const int32_t *host_offsets,
+                                   const int32_t *blocks, int64_t blocks_stride, double scale,
                                    void *out, void *workspace, size_t workspace_bytes,
                                    void *stream) {
   Geometry g;
   std::vector<int32_t> counts, lengths;
   if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (int rc = check_blocks(blocks, blocks_stride)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
   const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
-  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
+  return run_plan(plan, g, *q, *k, *v, blocks, blocks_stride, scale, contiguous_output(g, out), workspace,
                   static_cast<hipStream_t>(stream));
 }
 
@@ -766,12 +777,14 @@ size_t xinfer_batched_flash_attention_graph_workspace_size(const xinfer_view4 *q
 }
 
 int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
-                                         const int32_t *device_offsets, double scale, void *out, void *workspace,
+                                         const int32_t *device_offsets, const int32_t *blocks,
+                                         int64_t blocks_stride, double scale, void *out, void *workspace,
                                          size_t workspace_bytes, void *stream) {
   Geometry g;
   CapturePlan cp;
   if (int rc = check_capture(q, k, v, g, cp)) return rc;
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (int rc = check_blocks(blocks, blocks_stride)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr || device_offsets == nullptr) return XINFER_ERR_ARGUMENT;
   if (workspace_bytes < cp.bytes() || (cp.bytes() && workspace == nullptr)) return XINFER_ERR_WORKSPACE;
@@ -795,6 +808,8 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
   c.C = (int32_t)g.C;
   c.tok_item = cp.tok_item;
   c.row_records = cp.row_records;
+  c.blocks = blocks;
+  c.blocks_stride = blocks_stride;
   c.total_items = (int32_t)(g.B * g.Hkv * cp.splits_max);
   const hipStream_t s = static_cast<hipStream_t>(stream);
   if (launch_decode_capture(c, cp.dp, cp.qr, cp.rounds, cp.decode_blocks, s) != hipSuccess) return XINFER_ERR_LAUNCH;
@@ -806,13 +821,15 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
 }
 
 int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_view4 *k,
-                                           const xinfer_view4 *v, const int32_t *host_offsets, double scale,
+                                           const xinfer_view4 *v, const int32_t *host_offsets,
+                                           const int32_t *blocks, int64_t blocks_stride, double scale,
                                            void *out, void *stream) {
   static_assert(kScratchBytes == XINFER_NOALLOC_SCRATCH_BYTES, "scratch size of the C header");
   Geometry g;
   std::vector<int32_t> counts, lengths;
   if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (int rc = check_blocks(blocks, blocks_stride)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
   const Plan plan = cached_plan(g, counts, lengths);
@@ -821,23 +838,26 @@ int xinfer_batched_flash_attention_noalloc(const xinfer_view4 *q, const xinfer_v
   // the host-side name of the array).
   void *records = nullptr;
   if (plan.bytes() > 0 && scratch_pointer(&records) != hipSuccess) return XINFER_ERR_LAUNCH;
-  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), records,
+  return run_plan(plan, g, *q, *k, *v, blocks, blocks_stride, scale, contiguous_output(g, out), records,
                   static_cast<hipStream_t>(stream));
 }
 
 int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_view4 *v,
-                                       const int32_t *host_offsets, double scale, const xinfer_view4 *out,
+                                       const int32_t *host_offsets, const int32_t *blocks,
+                                       int64_t blocks_stride, double scale, const xinfer_view4 *out,
                                        void *workspace, size_t workspace_bytes, void *stream) {
   Geometry g;
   std::vector<int32_t> counts, lengths;
   if (int rc = check_batched(q, k, v, host_offsets, g, counts, lengths)) return rc;
   if (int rc = check_common(*q, *k, *v, scale)) return rc;
+  if (int rc = check_blocks(blocks, blocks_stride)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (int rc = check_output(g, out)) return rc;
   const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
-  return run_plan(plan, g, *q, *k, *v, scale, *out, workspace, static_cast<hipStream_t>(stream));
+  return run_plan(plan, g, *q, *k, *v, blocks, blocks_stride, scale, *out, workspace,
+                  static_cast<hipStream_t>(stream));
 }
 
 size_t xinfer_flash_attention_workspace_size(const xinfer_view4 *q, const xinfer_view4 *k,
@@ -859,7 +879,7 @@ int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const x
   const Plan plan = cached_plan(g, counts, lengths);
   if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
     return XINFER_ERR_WORKSPACE;
-  return run_plan(plan, g, *q, *k, *v, scale, contiguous_output(g, out), workspace,
+  return run_plan(plan, g, *q, *k, *v, nullptr, 0, scale, contiguous_output(g, out), workspace,
                   static_cast<hipStream_t>(stream));
 }
 

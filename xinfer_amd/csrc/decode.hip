@@ -76,6 +76,7 @@ constexpr int kDecodeRounds = kDecodeItemRounds;
 
 struct DecodeItem {
   int b, h, split, nsplit, cnt, L, t0, t1;
+  int kvb;    // cache row of the item's K/V: b, or b's page
   int first;  // item of split 0 of this (row, kv head)
   int64_t rec_begin;
 };
@@ -100,6 +101,7 @@ __device__ __forceinline__ DecodeItem locate_item(const RowSched &rs, int item, 
   it.split = local - it.h * rs.nsplit;
   it.nsplit = rs.nsplit;
   it.b = rs.batch;
+  it.kvb = rs.batch;
   it.cnt = rs.count;
   it.L = rs.length;
   it.t0 = it.split * tok_item;
@@ -163,8 +165,8 @@ __device__ __forceinline__ void issue_item(const DecodeParams &a, const DecodeIt
     if (round == 0 && part == 0) load_query(a, it, r, dc);  // wider groups load it in process_item
   }
   const uint32_t row_bytes_k = (uint32_t)(a.k.st * 2), row_bytes_v = (uint32_t)(a.v.st * 2);
-  const auto rk = buffer_rsrc(a.k.p + it.b * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
-  const auto rv = buffer_rsrc(a.v.p + it.b * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
+  const auto rk = buffer_rsrc(a.k.p + it.kvb * a.k.sb + (int64_t)it.h * a.k.sh, (uint32_t)it.t1 * row_bytes_k);
+  const auto rv = buffer_rsrc(a.v.p + it.kvb * a.v.sb + (int64_t)it.h * a.v.sh, (uint32_t)it.t1 * row_bytes_v);
   const int first = it.t0 + round * S::TOK_ROUND + wave * S::TOK_WAVE + slot;  // this lane's first key row
   // Chunks past D (padded head dims) are clamped into the row; their query
   // features are zero and their sums are not written.
@@ -612,10 +614,14 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   int nrows = a.nrows;
   DecodeParams p{a.q,          a.k,  a.v,  a.out, a.o_sb, a.o_sh,       a.o_st, a.part_o, a.part_ml,
                  a.scale_log2, a.D,  a.G,  a.T,   a.arrive_ctr, a.tag};
+  const int32_t *blocks = a.blocks;
+  int64_t blocks_stride = a.blocks_stride;
+  int kv_rows = a.kv_rows;
   asm volatile(""
                : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(nrows), XATTN_PIN_VIEW(p.q),
                  XATTN_PIN_VIEW(p.k), XATTN_PIN_VIEW(p.v), "+s"(p.out), "+s"(p.o_sb), "+s"(p.o_sh), "+s"(p.o_st),
-                 "+s"(p.part_o), "+s"(p.part_ml), "+s"(p.scale_log2), "+s"(p.D), "+s"(p.G), "+s"(p.T));
+                 "+s"(p.part_o), "+s"(p.part_ml), "+s"(p.scale_log2), "+s"(p.D), "+s"(p.G), "+s"(p.T),
+                 "+s"(blocks), "+s"(blocks_stride), "+s"(kv_rows));
   DecodeItem it;
   if (p.arrive_ctr == nullptr) {
     const int item = blockIdx.x;
@@ -632,8 +638,20 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
     const int h = 8 * hh + x, split = local - hh * rs.nsplit;
     it = locate_item(rs, rs.item_begin + h * rs.nsplit + split, ROUNDS * S::TOK_ROUND);
   }
+  // K/V rows: the page is read while the loads issued for row it.b are in
+  // flight; another page (never with the identity table) drains and reissues
+  // them.
+  const int raw_page = read_page(blocks, blocks_stride, it.b);
+  __builtin_amdgcn_sched_barrier(0);
   DecodeRegs<DP, QR> r;
   issue_item(p, it, r, wave, slot, dc);
+  __builtin_amdgcn_sched_barrier(0);
+  const int page = page_in_range(raw_page, kv_rows);
+  if (page != it.kvb) {
+    __builtin_amdgcn_s_waitcnt(0);
+    it.kvb = page;
+    issue_item(p, it, r, wave, slot, dc);
+  }
   process_item<DP, QR, ROUNDS>(p, it, r, sh, wave, lane, slot, dc);
 }
 
@@ -650,6 +668,7 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
   using S = DecodeShape<DP, QR>;
   __shared__ DecodeShared<DP, QR> sh;
   __shared__ int row_count[kMaxRows], row_length[kMaxRows], row_splits[kMaxRows], row_first[kMaxRows + 1];
+  __shared__ int row_page[kMaxRows];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int slot = lane / S::LPT, dc = lane % S::LPT;
   if (tid < c.B) {
@@ -658,6 +677,7 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
     row_count[tid] = count;
     row_length[tid] = length;
     row_splits[tid] = count == 0 ? 1 : (length + c.tok_item - 1) / c.tok_item;
+    row_page[tid] = page_in_range(c.blocks ? c.blocks[(int64_t)tid * c.blocks_stride] : tid, c.B);
   }
   __syncthreads();
   if (tid == 0) {
@@ -686,7 +706,8 @@ __global__ void __launch_bounds__(256) decode_capture_kernel(const CaptureArgs c
     rs.nsplit = row_splits[r];
     rs.ntiles = 1;
     rs.rec_begin = (int64_t)r * c.row_records;
-    const DecodeItem it = locate_item(rs, item, ROUNDS * S::TOK_ROUND);
+    DecodeItem it = locate_item(rs, item, ROUNDS * S::TOK_ROUND);
+    it.kvb = row_page[r];
     DecodeRegs<DP, QR> regs;
     issue_item(p, it, regs, wave, slot, dc);
     process_item<DP, QR, ROUNDS>(p, it, regs, sh, wave, lane, slot, dc);

@@ -234,6 +234,21 @@ struct RowLookup {
   }
 };
 
+// Cache row that holds row b's K/V under a page table (the reference's paged
+// FlashAttention call, compiler/common/kernels/attention.cpp:39-40, 68-70):
+// blocks[b * stride] clamped into [0, rows), so that no table can address
+// outside k/v; b itself without a table.  Kernels issue the read before their
+// first K/V loads (for row b) and clamp and compare it where those loads are
+// awaited anyway, reissuing them only when the page differs.  The read is a
+// scalar load (constant address space, block-uniform address), so waiting
+// for it never waits for vector loads.
+__device__ __forceinline__ int read_page(const int32_t *blocks, int64_t stride, int b) {
+  if (blocks == nullptr) return b;
+  typedef const __attribute__((address_space(4))) int32_t *table_ptr;
+  return ((table_ptr)blocks)[(int64_t)b * stride];
+}
+__device__ __forceinline__ int page_in_range(int page, int rows) { return min(max(page, 0), rows - 1); }
+
 // Row r's query count and KV length from the device offsets, clamped to the
 // ranges the host validates in the default mode (see CaptureArgs in kernel_args.h).
 __device__ __forceinline__ void capture_row(const CaptureArgs &c, int r, int &count, int &length) {

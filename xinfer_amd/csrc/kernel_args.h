@@ -49,6 +49,11 @@ struct AttnArgs {
   // launch the host makes.
   uint64_t *arrive_ctr;
   uint64_t tag;
+  // Page table (device, nullable): row r's K/V are k/v[page(r)], page(r) =
+  // blocks[r * blocks_stride] clamped into [0, kv_rows); null: k/v[r].
+  const int32_t *blocks;
+  int64_t blocks_stride;
+  int32_t kv_rows;  // size of k/v's batch dimension
 };
 
 // Merge of split partial records (merge.hip): one work item per query vector.
@@ -92,6 +97,8 @@ struct CaptureArgs {
   int32_t tok_item;          // keys per decode work item
   int32_t total_items;       // decode: items at capacity; merge: query vectors at capacity
   int64_t row_records;       // records per row at capacity: Hkv * ceil(C / tok_item) * T * G
+  const int32_t *blocks;     // page table as in AttnArgs (nullable), over the B rows of k/v
+  int64_t blocks_stride;
 };
 
 struct AppendArgs {

@@ -105,10 +105,13 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
       T = a.T;
   float c = a.scale_log2;
   View qv = a.q, kv = a.k, vv = a.v;
+  const int32_t *blocks = a.blocks;
+  int64_t blocks_stride = a.blocks_stride;
+  int kv_rows = a.kv_rows;
   asm volatile(""
                : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(run_begin), "+s"(run_end),
                  "+s"(nrows), "+s"(G), "+s"(D), "+s"(T), "+s"(c), XATTN_PIN_VIEW(qv), XATTN_PIN_VIEW(kv),
-                 XATTN_PIN_VIEW(vv));
+                 XATTN_PIN_VIEW(vv), "+s"(blocks), "+s"(blocks_stride), "+s"(kv_rows));
   const int item = run_begin + (int)(blockIdx.x / 8);
   if (item >= run_end) return;
   const RowSched rs = rows.find(a.rows, nrows, item);
@@ -146,9 +149,12 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   // the tile: key q / CHUNKS, slot q % CHUNKS, holding chunk slot ^ swizzle.
   // Chunks past D (padded head dims) repeat the row's last chunk: finite
   // values that only meet zero query features or unused output rows.
+  // The K/V rows are read from row b's cache, or from its page when a page
+  // table is given: the page is read once tiles 0 and 1 are loading from row
+  // b, and another page (never with the identity table) reloads them.
   const uint32_t k_row = (uint32_t)kv.st * 2, v_row = (uint32_t)vv.st * 2;
-  const u32x4 k_rsrc = buffer_words(kv.p + b * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
-  const u32x4 v_rsrc = buffer_words(vv.p + b * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
+  u32x4 k_rsrc = buffer_words(kv.p + b * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
+  u32x4 v_rsrc = buffer_words(vv.p + b * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
   uint32_t k_voff[LOADS], v_voff[LOADS];
 #pragma unroll
   for (int i = 0; i < LOADS; ++i) {
@@ -325,8 +331,20 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
     // compute: waves 0-3 tile t, waves 4-7 tile t+1, with no barrier between
     // the two, so the waves of a SIMD drift apart and overlap each other's
     // MFMA, LDS and softmax phases.
+    const int raw_page = read_page(blocks, blocks_stride, b);
+    __builtin_amdgcn_sched_barrier(0);
     if (ntile > 0) {
       issue_query();
+      issue(0, ks0);
+      if (ntile > 1) issue(1, ks0 + BN);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // Tiles 0 and 1 from the page, when it is not row b (block-uniform).
+    const int page = page_in_range(raw_page, kv_rows);
+    if (ntile > 0 && page != b) {
+      wait_loads_and_barrier<0>();
+      k_rsrc = buffer_words(kv.p + page * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
+      v_rsrc = buffer_words(vv.p + page * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
       issue(0, ks0);
       if (ntile > 1) issue(1, ks0 + BN);
     }

@@ -77,10 +77,13 @@ __global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a
       T = a.T;
   float c = a.scale_log2;
   View qv = a.q, kv = a.k, vv = a.v;
+  const int32_t *blocks = a.blocks;
+  int64_t blocks_stride = a.blocks_stride;
+  int kv_rows = a.kv_rows;
   asm volatile(""
                : XATTN_PIN_BEGINS(rows), XATTN_PIN_ROWSCHED(rows.first), "+s"(run_begin), "+s"(run_end),
                  "+s"(nrows), "+s"(G), "+s"(D), "+s"(T), "+s"(c), XATTN_PIN_VIEW(qv), XATTN_PIN_VIEW(kv),
-                 XATTN_PIN_VIEW(vv));
+                 XATTN_PIN_VIEW(vv), "+s"(blocks), "+s"(blocks_stride), "+s"(kv_rows));
   const int item = run_begin + (int)(blockIdx.x / 8);
   if (item >= run_end) return;
   const RowSched rs = rows.find(a.rows, nrows, item);
@@ -119,9 +122,12 @@ __global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a
   // key q / kChunks, slot q % kChunks, holding chunk slot ^ swizzle (clamped
   // into the row past D: finite values that meet zero query features or
   // unused output rows).  Every wave issues its share of every tile.
+  // K/V rows of row b's cache, or of its page when a page table is given:
+  // the page is read once tiles 0 and 1 are loading from row b, and another
+  // page (never with the identity table) reloads them (prologue).
   const uint32_t k_row = (uint32_t)kv.st * 2, v_row = (uint32_t)vv.st * 2;
-  const u32x4 k_rsrc = buffer_words(kv.p + b * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
-  const u32x4 v_rsrc = buffer_words(vv.p + b * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
+  u32x4 k_rsrc = buffer_words(kv.p + b * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
+  u32x4 v_rsrc = buffer_words(vv.p + b * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
   uint32_t k_voff[kLoads], v_voff[kLoads];
 #pragma unroll
   for (int i = 0; i < kLoads; ++i) {
@@ -154,10 +160,23 @@ __global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a
   };
   // Prologue: Q (producers), tiles 0 and 1; wait for Q and tile 0.
   auto prologue = [&]() {
+    const int raw_page = read_page(blocks, blocks_stride, b);
+    __builtin_amdgcn_sched_barrier(0);
     if (ntile > 0) issue(0);
     if (ntile > 1) issue(1);
+    __builtin_amdgcn_sched_barrier(0);
     if (ntile > 1) wait_loads_and_barrier<2 * kLoads>();
     else wait_loads_and_barrier<0>();
+    const int page = page_in_range(raw_page, kv_rows);
+    if (page != b) {  // block-uniform: drain, then tiles 0 and 1 from the page
+      wait_loads_and_barrier<0>();
+      k_rsrc = buffer_words(kv.p + page * kv.sb + (int64_t)h * kv.sh, (uint32_t)ks1 * k_row);
+      v_rsrc = buffer_words(vv.p + page * vv.sb + (int64_t)h * vv.sh, (uint32_t)ks1 * v_row);
+      if (ntile > 0) issue(0);
+      if (ntile > 1) issue(1);
+      if (ntile > 1) wait_loads_and_barrier<2 * kLoads>();
+      else wait_loads_and_barrier<0>();
+    }
   };
   u32x4 *const wbuf = reinterpret_cast<u32x4 *>(reinterpret_cast<char *>(smem) + kWeightsAt);
   float *const fbuf = reinterpret_cast<float *>(reinterpret_cast<char *>(smem) + kFactorAt);

@@ -95,10 +95,12 @@ at::Tensor batched_attention(const at::Tensor &q, const at::Tensor &k, const at:
   auto output = bthd ? at::empty({q.size(0), q.size(2), q.size(1), q.size(3)}, q.options())
                      : at::empty(q.sizes(), q.options());
   if (batch == 0 || q.size(2) == 0) return output;
-  // Row r's KV lives in k[r]/v[r]: `blocks` is the identity page table built by
-  // batched_attention_metadata and needs no read.  Copy only what the kernels
-  // cannot read in place, as the reference does (:58-61, :108-114); a copy of
-  // the longest populated prefix covers every key any row reads.
+  // Row r's KV lives in k[page]/v[page], page = blocks[r] when the capacity
+  // is a multiple of 256 (the reference's paged call, :39-40, :56-58, :68-70),
+  // else k[r]/v[r].  The kernels read the table on the device.  Copy only
+  // what the kernels cannot read in place, as the reference does (:58-61,
+  // :108-114); a copy of the longest populated prefix covers every key any
+  // row reads, in every row of the batch dimension.
   auto query = query_layout(q) ? q : q.contiguous();
   auto key = kernel_layout(k) ? k : k.narrow(2, 0, max_length).contiguous();
   auto value = kernel_layout(v) ? v : v.narrow(2, 0, max_length).contiguous();
@@ -107,15 +109,16 @@ at::Tensor batched_attention(const at::Tensor &q, const at::Tensor &k, const at:
     value = v.narrow(2, 0, max_length).contiguous();
   }
   auto qv = view_of(query), kv = view_of(key), vv = view_of(value);
+  const int32_t *pages = k.size(2) % 256 == 0 ? static_cast<const int32_t *>(blocks.data_ptr()) : nullptr;
   const size_t bytes = xinfer_batched_flash_attention_workspace_size(&qv, &kv, cuq);
   auto workspace = at::empty({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
   if (bthd) {
     auto ov = view_of(output.transpose(1, 2));
-    check_status(xinfer_batched_flash_attention_out(&qv, &kv, &vv, cuq, scale, &ov, workspace.data_ptr(), bytes,
-                                                    current_stream(q)));
+    check_status(xinfer_batched_flash_attention_out(&qv, &kv, &vv, cuq, pages, blocks.stride(0), scale, &ov,
+                                                    workspace.data_ptr(), bytes, current_stream(q)));
   } else {
-    check_status(xinfer_batched_flash_attention(&qv, &kv, &vv, cuq, scale, output.data_ptr(),
-                                                workspace.data_ptr(), bytes, current_stream(q)));
+    check_status(xinfer_batched_flash_attention(&qv, &kv, &vv, cuq, pages, blocks.stride(0), scale,
+                                                output.data_ptr(), workspace.data_ptr(), bytes, current_stream(q)));
   }
   return output;
 }
@@ -170,9 +173,10 @@ at::Tensor batched_flash_attention_graph(const at::Tensor &q, const at::Tensor &
   auto qv = view_of(query), kv = view_of(key), vv = view_of(value);
   const size_t bytes = xinfer_batched_flash_attention_graph_workspace_size(&qv, &kv);
   auto workspace = at::empty({static_cast<int64_t>(bytes)}, q.options().dtype(at::kByte));
+  const int32_t *pages = k.size(2) % 256 == 0 ? static_cast<const int32_t *>(blocks.data_ptr()) : nullptr;
   check_status(xinfer_batched_flash_attention_graph(&qv, &kv, &vv, static_cast<const int32_t *>(cuda_offsets.data_ptr()),
-                                                    scale, output.data_ptr(), workspace.data_ptr(), bytes,
-                                                    current_stream(q)));
+                                                    pages, blocks.stride(0), scale, output.data_ptr(),
+                                                    workspace.data_ptr(), bytes, current_stream(q)));
   return output;
 }
 
