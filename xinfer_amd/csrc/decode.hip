@@ -647,7 +647,7 @@ __global__ void __launch_bounds__(256) decode_kernel(const AttnArgs a) {
   issue_item(p, it, r, wave, slot, dc);
   __builtin_amdgcn_sched_barrier(0);
   const int page = page_in_range(raw_page, kv_rows);
-  if (page != it.kvb) {
+  if (__builtin_expect(page != it.kvb, 0)) {
     __builtin_amdgcn_s_waitcnt(0);
     it.kvb = page;
     issue_item(p, it, r, wave, slot, dc);
