@@ -6,7 +6,6 @@ library per process) without touching the real operator registry.
 """
 
 import os
-from pathlib import Path
 from types import SimpleNamespace
 from unittest.mock import Mock, patch
 

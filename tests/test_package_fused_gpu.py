@@ -27,6 +27,7 @@ import pytest
 import torch
 from torch.fx.experimental import _config as symbolic_config
 
+from xinfer_amd.adapters import MAX_BATCH_SIZE, MAX_PREFILL
 from attn_helpers import log
 
 pytestmark = pytest.mark.gpu
@@ -85,10 +86,10 @@ def export_step(step, kind):
     starts = [16 + 8 * row for row in range(batch_size)]
     counts = [max(1, width // (row + 1)) for row in range(batch_size)]
     inputs = step_inputs(batch_size, width, starts, counts)
-    batch = torch.export.Dim("batch", min=1, max=8)
+    batch = torch.export.Dim("batch", min=1, max=MAX_BATCH_SIZE)
     token_shape = {0: batch}
     if kind == "prefill":
-        token_shape[1] = torch.export.Dim("tokens", min=2, max=512)
+        token_shape[1] = torch.export.Dim("tokens", min=2, max=MAX_PREFILL)
     per_layer = tuple(token_shape for _ in range(LAYERS))
     shapes = (per_layer, per_layer, per_layer, token_shape, token_shape, token_shape,
               tuple({0: batch} for _ in range(2 * LAYERS)), {0: batch}, {0: batch})

@@ -54,6 +54,7 @@ import pytest
 import torch
 from torch.fx.experimental import _config as symbolic_config
 
+from xinfer_amd.adapters import MAX_BATCH_SIZE, MAX_PREFILL
 from attn_helpers import log
 from model_steps import CAPACITY, LAYERS, VARIANTS, build_model, step_inputs
 
@@ -76,10 +77,10 @@ def export_step(step, kind):
               cache,
               torch.tensor([start + count for start, count in zip(starts, counts)], dtype=torch.int32),
               torch.tensor(counts, dtype=torch.int32))
-    batch = torch.export.Dim("batch", min=1, max=8)
+    batch = torch.export.Dim("batch", min=1, max=MAX_BATCH_SIZE)
     token_shape = {0: batch}
     if kind == "prefill":
-        token_shape[1] = torch.export.Dim("tokens", min=2, max=512)
+        token_shape[1] = torch.export.Dim("tokens", min=2, max=MAX_PREFILL)
     shapes = (token_shape, token_shape, tuple({0: batch} for _ in cache), {0: batch}, {0: batch})
     with symbolic_config.patch(backed_size_oblivious=True):
         exported = torch.export.export(step, inputs, dynamic_shapes=shapes, strict=False)

@@ -33,6 +33,8 @@ import torch
 
 from .attention import batched_attention_metadata, load_attention_ops, require
 
+# Export bounds of the model steps (compiler/qwen35/config.py:8-9): batch and
+# prefill tokens per step.
 MAX_PREFILL = 512
 MAX_BATCH_SIZE = 8
 
