@@ -230,3 +230,44 @@ def test_fused_step_in_graph_replays(gpu_ops):
         torch.cuda.synchronize()
         assert torch.equal(replayed[0].view(torch.int16), eager.view(torch.int16)), replay
         assert all(torch.equal(a, b) for a, b in zip(replayed[1:], caches)), replay
+
+
+@torch.inference_mode()
+def test_page_table_through_c_abi(capi, gpu_ops):
+    """The C entry points with a page table (device pointer and row stride):
+    the workspace entry point and the allocation-free one give the torch
+    operator's bits for a permuted table viewed with row stride 2."""
+    counts, lengths, capacity, dim = [1, 40, 0, 1], [700, 300, 5, 1024], 1024, 128
+    log(f"C ABI page table: counts={counts} lengths={lengths} C={capacity}")
+    generator = torch.Generator().manual_seed(5)
+    q = torch.randn(4, 16, 40, dim, generator=generator).to(torch.bfloat16).cuda()
+    k = torch.randn(4, 8, capacity, dim, generator=generator).to(torch.bfloat16).cuda()
+    v = torch.randn(4, 8, capacity, dim, generator=generator).to(torch.bfloat16).cuda()
+    host, cu, _ = batched_attention_metadata(
+        torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
+    table = torch.tensor([[2, 7], [0, 7], [3, 7], [1, 7]], dtype=torch.int32).cuda()[:, :1]
+    assert table.stride(0) == 2
+    expected = gpu_ops.batched_flash_attention(q, k, v, host, cu, table, dim**-0.5)
+    qv, kv, vv = view(q), view(k), view(v)
+    offsets = host.contiguous()
+    host_ptr = ctypes.cast(offsets.data_ptr(), ctypes.POINTER(ctypes.c_int32))
+    pages, stride_ = ctypes.c_void_p(table.data_ptr()), ctypes.c_int64(table.stride(0))
+    size = capi.xinfer_batched_flash_attention_workspace_size(ctypes.byref(qv), ctypes.byref(kv), host_ptr)
+    workspace = torch.empty(max(size, 1), dtype=torch.uint8, device="cuda")
+    out = torch.empty_like(q)
+    status = capi.xinfer_batched_flash_attention(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, pages, stride_, ctypes.c_double(dim**-0.5),
+        ctypes.c_void_p(out.data_ptr()), ctypes.c_void_p(workspace.data_ptr()), ctypes.c_size_t(size), stream())
+    assert status == 0, capi.xinfer_status_string(status)
+    free = torch.empty_like(q)
+    status = capi.xinfer_batched_flash_attention_noalloc(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(vv), host_ptr, pages, stride_, ctypes.c_double(dim**-0.5),
+        ctypes.c_void_p(free.data_ptr()), stream())
+    assert status == 0, capi.xinfer_status_string(status)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), expected.view(torch.int16))
+    assert torch.equal(free.view(torch.int16), expected.view(torch.int16))
+    moved = gpu_ops.batched_flash_attention(q, k[[2, 0, 3, 1]].contiguous(), v[[2, 0, 3, 1]].contiguous(), host, cu,
+                                            torch.arange(4, dtype=torch.int32, device="cuda").view(4, 1), dim**-0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), moved.view(torch.int16))
