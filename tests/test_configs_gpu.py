@@ -11,8 +11,18 @@ GPU and the CPU oracle).  Gates:
 * the error is no worse than the reference path's own bf16 error: torch SDPA
   on bf16 tensors with the explicit lower-right mask (the adapted eager
   attention) on the device's flash-family kernels, measured on the same rows
-  and inputs.  Both the worst and the mean absolute error must be at or below
-  the reference path's.
+  and inputs.  On every input the bench times, both the worst and the mean
+  absolute error must be at or below the reference path's.
+
+More draws of the two prefill configurations (cfg2 seeds 0-5, cfg5 seeds
+0-3) are held to the same bar across draws: per draw the mean absolute error
+at or below the reference path's and the absolute gates; per configuration
+the worst error over its draws at or below the reference path's worst over
+the same draws.  Per draw, the worst error of both paths is an output
+element about half a bf16 step from its exact value, whose side of a
+rounding midpoint the weights' bf16 rounding decides in either path, so it
+is compared over the draws rather than draw by draw; each draw's ratio is
+logged.
 """
 
 import numpy as np
@@ -92,9 +102,9 @@ CASES = [(1, 0), (2, 0), (2, 1), (3, 0), (3, 1), (3, 2), (3, 3), (3, 4), (3, 5),
          (5, 0), (5, 1)]
 
 
-@pytest.mark.parametrize("index,seed", CASES, ids=[f"cfg{i}_seed{s}" for i, s in CASES])
-@torch.inference_mode()
-def test_config_parity(gpu_ops, index, seed):
+def draw_errors(gpu_ops, index, seed):
+    """(ours, reference path) error statistics of one draw against the float64 oracle,
+    after checking the appended caches bit for bit."""
     w = workloads.config(index, seed)
     log(f"config {w.name} seed {seed}: B={w.batch} Hq={w.heads} Hkv={w.kv_heads} D={w.dim} C={w.capacity} "
         f"counts={w.counts} lengths={w.lengths}")
@@ -122,15 +132,40 @@ def test_config_parity(gpu_ops, index, seed):
         worst["source"] = source
         worst["ref_max_abs"] = max(worst["ref_max_abs"], float(ref_delta.max()))
         worst["ref_sum_abs"] += float(ref_delta.sum())
-    mean_abs = worst["sum_abs"] / worst["n"]
-    ref_mean = worst["ref_sum_abs"] / worst["n"]
-    log(f"  errors vs float64 oracle: max_abs={worst['max_abs']:.3e} mean_abs={mean_abs:.3e}; "
-        f"bf16 reference path ({worst['source']}): max_abs={worst['ref_max_abs']:.3e} mean_abs={ref_mean:.3e}; "
-        f"ratios max {worst['max_abs'] / worst['ref_max_abs']:.3f} mean {mean_abs / ref_mean:.3f}")
-    assert worst["max_abs"] <= MAX_ABS
-    assert mean_abs <= MEAN_ABS
-    assert mean_abs <= BF16_SLACK * ref_mean
-    assert worst["max_abs"] <= BF16_SLACK * worst["ref_max_abs"]
+    stats = dict(max_abs=worst["max_abs"], mean_abs=worst["sum_abs"] / worst["n"], ref_max_abs=worst["ref_max_abs"],
+                 ref_mean_abs=worst["ref_sum_abs"] / worst["n"], source=worst["source"])
+    log(f"  errors vs float64 oracle: max_abs={stats['max_abs']:.3e} mean_abs={stats['mean_abs']:.3e}; "
+        f"bf16 reference path ({stats['source']}): max_abs={stats['ref_max_abs']:.3e} "
+        f"mean_abs={stats['ref_mean_abs']:.3e}; ratios max {stats['max_abs'] / stats['ref_max_abs']:.3f} "
+        f"mean {stats['mean_abs'] / stats['ref_mean_abs']:.3f}")
+    assert stats["max_abs"] <= MAX_ABS
+    assert stats["mean_abs"] <= MEAN_ABS
+    return stats
+
+
+@pytest.mark.parametrize("index,seed", CASES, ids=[f"cfg{i}_seed{s}" for i, s in CASES])
+@torch.inference_mode()
+def test_config_parity(gpu_ops, index, seed):
+    stats = draw_errors(gpu_ops, index, seed)
+    assert stats["mean_abs"] <= BF16_SLACK * stats["ref_mean_abs"]
+    assert stats["max_abs"] <= BF16_SLACK * stats["ref_max_abs"]
+
+
+# Prefill configurations and the draws held to the bar across draws.
+DRAWS = {2: range(6), 5: range(4)}
+
+
+@pytest.mark.parametrize("index", sorted(DRAWS), ids=[f"cfg{i}" for i in sorted(DRAWS)])
+@torch.inference_mode()
+def test_prefill_draws_against_the_reference_error(gpu_ops, index):
+    draws = [draw_errors(gpu_ops, index, seed) for seed in DRAWS[index]]
+    for seed, stats in zip(DRAWS[index], draws):
+        assert stats["mean_abs"] <= BF16_SLACK * stats["ref_mean_abs"], (index, seed, stats)
+    ours, reference = max(d["max_abs"] for d in draws), max(d["ref_max_abs"] for d in draws)
+    log(f"cfg{index} seeds {list(DRAWS[index])}: worst max_abs {ours:.3e} against the reference path's "
+        f"{reference:.3e} (ratio {ours / reference:.3f}); per-draw max ratios "
+        f"{[round(d['max_abs'] / d['ref_max_abs'], 3) for d in draws]}")
+    assert ours <= BF16_SLACK * reference
 
 
 @torch.inference_mode()
