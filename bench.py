@@ -650,17 +650,17 @@ def measure_gemv(replays=20, per_graph=50):
     return results
 
 
-def measure_graph_decode(steps, warmup):
+def compare_graph_mode(cases, steps, warmup, label):
     """The graph-capture operator (lengths read on the device, launch sized
     for the capacity) against the default operator (launch planned from host
-    lengths) on the decode workloads: attention-op time of each, from HIP
+    lengths) on the (config, seed) cases: attention-op time of each, from HIP
     events around graph replays as in the main line."""
     import torch
 
     from xinfer_amd import workloads
 
     results = []
-    for index, seed in [(3, s) for s in range(8)] + [(4, 0)]:
+    for index, seed in cases:
         w = workloads.config(index, seed)
         inputs = workloads.make_inputs(w)
         times = {}
@@ -675,11 +675,22 @@ def measure_graph_decode(steps, warmup):
         results.append({"workload": w.name, "default_us": round(times["default"] * 1e6, 2),
                         "graph_us": round(times["graph"] * 1e6, 2),
                         "graph_GBs": round(w.kv_bytes() / times["graph"] / 1e9, 1)})
-        log(f"[bench] graph-capture decode {w.name}: default {times['default'] * 1e6:.1f} us, "
+        log(f"[bench] graph-capture {label} {w.name}: default {times['default'] * 1e6:.1f} us, "
             f"graph mode {times['graph'] * 1e6:.1f} us")
+    return results
+
+
+def measure_graph_decode(steps, warmup):
+    """compare_graph_mode on the decode workloads, cfg3 seeds 0-7 and cfg4."""
+    results = compare_graph_mode([(3, s) for s in range(8)] + [(4, 0)], steps, warmup, "decode")
     default = sum(r["default_us"] for r in results if r["workload"].startswith("cfg3_"))
     graph = sum(r["graph_us"] for r in results if r["workload"].startswith("cfg3_"))
     return {"graph_decode": results, "cfg3_seeds_0_7_us": {"default": round(default, 2), "graph": round(graph, 2)}}
+
+
+def measure_graph_prefill(steps, warmup):
+    """compare_graph_mode on the prefill workloads cfg1, cfg2 and cfg5."""
+    return {"graph_prefill": compare_graph_mode([(1, 0), (2, 0), (5, 0)], steps, warmup, "prefill")}
 
 
 COPY_PROBE_BYTES = 256 << 20
@@ -756,6 +767,8 @@ def main():
                         help="comma-separated workloads INDEX[:SEED] (e.g. 2,5,3:1) to time alone; prints their results")
     parser.add_argument("--graph-decode", action="store_true",
                         help="only time the graph-capture operator against the default one on the decode workloads")
+    parser.add_argument("--graph-prefill", action="store_true",
+                        help="only time the graph-capture operator against the default one on cfg1, cfg2 and cfg5")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-budget", type=float, default=4.0, help="seconds per CPU-baseline leg")
     parser.add_argument("--eager", action="store_true", help="launch steps eagerly instead of graph replay")
@@ -794,6 +807,9 @@ def main():
         return
     if args.graph_decode:
         print(json.dumps(measure_graph_decode(args.steps, args.warmup)), flush=True)
+        return
+    if args.graph_prefill:
+        print(json.dumps(measure_graph_prefill(args.steps, args.warmup)), flush=True)
         return
     with_cpu = not args.no_cpu_baseline
     if args.only:

@@ -44,7 +44,7 @@ enum {
   XINFER_ERR_ROPE_SHAPE = 15,     /* xinfer_qk_norm_rope_append shapes (no reference message) */
   XINFER_ERR_EPS = 16,            /* RMSNorm epsilon not finite and >= 0 (no reference message) */
   XINFER_ERR_SCRATCH = 17,        /* the call needs more than XINFER_NOALLOC_SCRATCH_BYTES of scratch */
-  XINFER_ERR_CAPTURE_ROWS = 18    /* graph-capture mode: T * Hq/Hkv > 8 or more than 64 rows */
+  XINFER_ERR_CAPTURE_ROWS = 18    /* graph-capture mode: more than 64 rows */
 };
 
 /* A strided rank-4 view of bf16 device memory, [batch, heads, sequence, dim].
@@ -114,17 +114,20 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
                                        size_t workspace_bytes, void *stream);
 
 /* Graph-capture ("capture once, replay every step") variant of
- * xinfer_batched_flash_attention for decode batches.  No counterpart in the
- * reference, which leaves graph capture to future runtime work (PLAN.md:35-37):
- * it is for serving loops that capture one decode step in a HIP graph and
- * replay it while the lengths change.  device_offsets is the DEVICE copy of
+ * xinfer_batched_flash_attention.  No counterpart in the reference, which
+ * leaves graph capture to future runtime work (PLAN.md:35-37): it is for
+ * serving loops that capture one step in a HIP graph and replay it while the
+ * lengths change.  device_offsets is the DEVICE copy of
  * the cumulative offsets (int32 [2][B+1], batched_attention_metadata's
  * cuda_offsets); the kernels read every row's count and length from it when
  * they run, so nothing about the launch depends on host lengths and a
  * captured call stays valid after the caller rewrites device_offsets in place
  * (and the page table, read the same way).
  * The workspace size depends on the shapes only (all rows at capacity C).
- * Rows must take the decode path: T * (Hq/Hkv) <= 8, and B <= 64
+ * Shapes with T * (Hq/Hkv) <= 8 take the decode kernels; larger ones take the
+ * prefill kernels, whose work list and key splits a one-wave plan kernel
+ * writes into the workspace from device_offsets at run time (the split length
+ * is chosen on the host for rows of T queries over C keys).  B <= 64
  * (XINFER_ERR_CAPTURE_ROWS otherwise).  Device lengths are not validated on
  * the host: counts are clamped to [0, T] and lengths to [max(count, 1), C], so
  * bad values give wrong rows but never an access outside the tensors.

@@ -86,10 +86,11 @@ def check_oracle(out, q, k, v, rows, scale):
             assert errors["max_abs"] <= MAX_ABS and errors["mean_abs"] <= MEAN_ABS, (r, errors)
 
 
-@pytest.mark.parametrize("name", list(SHAPES))
-@torch.inference_mode()
-def test_one_captured_step_replays_every_length_set(gpu_ops, name):
-    heads, kv_heads, dim, tokens, capacity, length_sets = SHAPES[name]
+def replay_length_sets(gpu_ops, name, shape):
+    """Capture append + graph attention once for `shape`, then replay it over
+    every length set twice, each replay checked against the eager operators,
+    the float64 oracle and the default operator."""
+    heads, kv_heads, dim, tokens, capacity, length_sets = shape
     batch = len(length_sets[0])
     scale = dim**-0.5
     generator = torch.Generator().manual_seed(sum(map(ord, name)))
@@ -138,7 +139,7 @@ def test_one_captured_step_replays_every_length_set(gpu_ops, name):
 
     for round_ in range(2):
         for rows in length_sets:
-            log(f"graph decode {name} round {round_}: rows={rows}")
+            log(f"graph step {name} round {round_}: rows={rows}")
             set_step(rows)
             k_before, v_before = k.clone(), v.clone()
             torch.cuda.synchronize()
@@ -159,10 +160,16 @@ def test_one_captured_step_replays_every_length_set(gpu_ops, name):
             assert float(delta.max()) <= MAX_ABS and float(delta.mean()) <= MEAN_ABS
 
 
+@pytest.mark.parametrize("name", list(SHAPES))
 @torch.inference_mode()
-def test_graph_mode_rejects_prefill_rows(gpu_ops):
-    q = torch.zeros(1, 16, 16, 128, device="cuda", dtype=torch.bfloat16)
-    k = torch.zeros(1, 8, 256, 128, device="cuda", dtype=torch.bfloat16)
-    host, cu, blocks = metadata([(16, 32)])
-    with pytest.raises(RuntimeError, match="Graph-capture attention takes decode rows"):
+def test_one_captured_step_replays_every_length_set(gpu_ops, name):
+    replay_length_sets(gpu_ops, name, SHAPES[name])
+
+
+@torch.inference_mode()
+def test_graph_mode_rejects_more_than_64_rows(gpu_ops):
+    q = torch.zeros(65, 16, 1, 128, device="cuda", dtype=torch.bfloat16)
+    k = torch.zeros(65, 8, 256, 128, device="cuda", dtype=torch.bfloat16)
+    host, cu, blocks = metadata([(1, 32)] * 65)
+    with pytest.raises(RuntimeError, match="Graph-capture attention takes at most 64 rows"):
         gpu_ops.batched_flash_attention_graph(q, k, k, host, cu, blocks, 128**-0.5)

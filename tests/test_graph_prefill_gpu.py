@@ -1,0 +1,55 @@
+"""A prefill (chunked) step captured once in a HIP graph and replayed while the lengths change.
+
+For shapes with more than 8 query vectors per KV head (T * Hq/Hkv > 8),
+xinfer::batched_flash_attention_graph plans on the device: a one-wave plan
+kernel reads every row's query count and KV length from cuda_offsets and
+writes the prefill kernel's and the merge kernel's arguments into the
+workspace (prefill.hip: prefill_capture_plan_kernel), with the split size the
+host planner gives the shapes at capacity; the prefill and merge kernels then
+read their arguments from there, over grids sized for every row at capacity
+(blocks past the planned items exit).  Every row takes the prefill kernel,
+including rows with one query and rows without queries (which only zero
+their outputs).
+
+As for decode (tests/test_graph_decode_gpu.py): the append and the attention
+are captured once, and every replay over the length sets below must equal,
+bit for bit, the same operators launched eagerly, stay within the float64
+oracle's gates, and agree with the default operator (host-planned, other
+splits) within the same gates.  Shapes: Qwen3 chunks (G = 2, two query tiles
+per row, split rows merged), Qwen3.5 chunks (D = 256, G = 4), head dim 64
+with G = 1 (one tile), and a capacity that needs no split (no merge launch).
+"""
+
+import pytest
+import torch
+
+from test_graph_decode_gpu import replay_length_sets
+
+pytestmark = pytest.mark.gpu
+
+# (Hq, Hkv, D, T, capacity, length sets: per row (count, length))
+SHAPES = {
+    "qwen3_chunks": (16, 8, 128, 128, 4096, [
+        [(128, 2048), (64, 1000), (1, 300), (0, 5)],
+        [(128, 4096), (128, 128), (100, 3000), (2, 2)],
+        [(1, 1), (128, 4000), (17, 700), (128, 1024)],
+    ]),
+    "qwen35_chunks": (16, 4, 256, 64, 2048, [
+        [(64, 2048), (1, 77), (33, 1500), (0, 3)],
+        [(64, 64), (64, 2000), (2, 2), (64, 1024)],
+    ]),
+    "d64_group1": (8, 8, 64, 40, 1024, [
+        [(40, 1024), (5, 500), (40, 40), (1, 1)],
+        [(0, 9), (40, 900), (39, 1000), (12, 12)],
+    ]),
+    "no_split": (8, 4, 128, 16, 512, [
+        [(16, 512), (1, 1), (16, 16), (0, 2)],
+        [(3, 300), (16, 100), (16, 500), (8, 9)],
+    ]),
+}
+
+
+@pytest.mark.parametrize("name", list(SHAPES))
+@torch.inference_mode()
+def test_one_captured_prefill_step_replays_every_length_set(gpu_ops, name):
+    replay_length_sets(gpu_ops, name, SHAPES[name])

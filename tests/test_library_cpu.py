@@ -248,7 +248,7 @@ def test_graph_mode_shapes_and_workspace(lib):
     assert workspace(8, 16384) == records_bytes(8, 16384 // 512)   # 8192 one-round items -> four rounds
     assert workspace(1, 4096) == records_bytes(1, 4096 // 128)     # 256 one-round items
     assert workspace(16, 16384) == records_bytes(16, 16384 // 128)  # 4096 four-round items: one round
-    assert lib.xinfer_status_string(18).decode().startswith("Graph-capture attention takes decode rows")
+    assert lib.xinfer_status_string(18).decode() == "Graph-capture attention takes at most 64 rows"
 
     def graph(qv, kv):
         return lib.xinfer_batched_flash_attention_graph(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),
@@ -256,7 +256,7 @@ def test_graph_mode_shapes_and_workspace(lib):
                                                         ctypes.c_double(0.1), ctypes.c_void_p(1 << 20), None,
                                                         ctypes.c_size_t(0), None)
 
-    assert graph(view([1, 16, 5, 128]), view([1, 8, 256, 128])) == 18   # 10 query vectors per KV head
+    assert graph(view([1, 16, 5, 128]), view([1, 8, 256, 128])) == 10   # prefill shapes: no workspace given
     assert graph(view([65, 16, 1, 128]), view([65, 8, 256, 128])) == 18
     assert graph(view([1, 16, 1, 128]), view([1, 8, 256, 128])) == 10   # no workspace given
     assert lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(view([1, 16, 1, 128])),

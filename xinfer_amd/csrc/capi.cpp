@@ -656,9 +656,17 @@ int check_batched(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
 struct CapturePlan {
   int dp = 0, qr = 1, rounds = 1, tok_item = 0, splits_max = 0, decode_blocks = 0;
   int64_t row_records = 0, records = 0;
-  size_t part_ml_offset() const { return (size_t)((records * dp_d * 4 + 255) / 256 * 256); }
-  size_t bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
   int64_t dp_d = 0;  // the head dim D (records hold D floats)
+  // Prefill shapes (T * Hq/Hkv > 8): every row takes the prefill kernel,
+  // planned on the device; the workspace also holds the prefill and merge
+  // arguments the plan kernel writes.
+  bool prefill = false;
+  int64_t split_keys = 0, items_max = 0, vectors_max = 0;
+  size_t part_ml_offset() const { return (size_t)((records * dp_d * 4 + 255) / 256 * 256); }
+  size_t records_bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
+  size_t attn_offset() const { return (records_bytes() + 255) / 256 * 256; }
+  size_t merge_offset() const { return attn_offset() + (sizeof(AttnArgs) + 255) / 256 * 256; }
+  size_t bytes() const { return prefill ? merge_offset() + sizeof(MergeArgs) : records_bytes(); }
 };
 // Decode blocks of a capture launch: every item of the capacity layout, at
 // most eight per CU of the 256.  With one-round items the blocks take the
@@ -678,9 +686,22 @@ int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
     return XINFER_ERR_QKV_SHAPES;
   if (int rc = check_heads_and_dim(g)) return rc;
   const int64_t G = g.Hq / g.Hkv;
-  if (g.T * G > kDecodeMaxQueryVectors || g.B > kMaxRows) return XINFER_ERR_CAPTURE_ROWS;
+  if (g.B > kMaxRows) return XINFER_ERR_CAPTURE_ROWS;
   cp.dp = padded_dim(g.D);
   cp.dp_d = g.D;
+  if (g.T * G > kDecodeMaxQueryVectors) {
+    // Prefill shapes: the split size of the host plan with every row at T
+    // queries and C keys; the device plan gives each row at most
+    // tiles x splits items of that size.
+    cp.prefill = true;
+    const std::vector<int32_t> counts((size_t)g.B, (int32_t)g.T), lengths((size_t)g.B, (int32_t)g.C);
+    cp.split_keys = choose_split_keys(g, counts, lengths, (int)G, cp.dp);
+    cp.splits_max = prefill_splits(g.C, cp.split_keys);
+    cp.items_max = g.B * g.Hkv * ceil_div(g.T * G, kPrefillTileQ) * cp.splits_max;
+    cp.vectors_max = g.B * g.Hkv * g.T * G;
+    cp.records = cp.splits_max > 1 ? cp.items_max * kPrefillTileQ : 0;
+    return XINFER_OK;
+  }
   cp.qr = pow2_at_least((int)std::max<int64_t>(1, g.T * G));
   const int tok_round = decode_tokens_per_item(cp.dp, cp.qr);
   const int64_t one_round_items = g.B * g.Hkv * ceil_div(g.C, tok_round);
@@ -734,8 +755,7 @@ const char *xinfer_status_string(int status) {
       return "Expected q [B,Hq,T,D], key/value [B,Hkv,T,D] and cos/sin [B,1,T,D] with D in {64,128,256}";
     case XINFER_ERR_EPS: return "RMSNorm epsilon must be finite and non-negative";
     case XINFER_ERR_CAPTURE_ROWS:
-      return "Graph-capture attention takes decode rows: at most 8 query vectors per KV head (T * Hq/Hkv) "
-             "and 64 rows";
+      return "Graph-capture attention takes at most 64 rows";
     case XINFER_ERR_SCRATCH:
       return "Attention needs more split-record scratch than the allocation-free entry point holds (32 MiB)";
     default: return "Unknown xinfer status";
@@ -812,6 +832,21 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
   c.blocks_stride = blocks_stride;
   c.total_items = (int32_t)(g.B * g.Hkv * cp.splits_max);
   const hipStream_t s = static_cast<hipStream_t>(stream);
+  if (cp.prefill) {
+    char *ws = static_cast<char *>(workspace);
+    PrefillPlanArgs pp{};
+    pp.c = c;
+    pp.attn = reinterpret_cast<AttnArgs *>(ws + cp.attn_offset());
+    pp.merge = reinterpret_cast<MergeArgs *>(ws + cp.merge_offset());
+    pp.split_keys = (int32_t)cp.split_keys;
+    // Equal-count XCD runs of at most items_max items: 8 runs of at most
+    // ceil(items_max / 8) blocks each.
+    const unsigned blocks8 = (unsigned)(8 * ceil_div(cp.items_max, 8));
+    if (launch_prefill_capture(pp, cp.dp, blocks8, s) != hipSuccess) return XINFER_ERR_LAUNCH;
+    if (cp.splits_max > 1 && launch_merge_dev(pp.merge, cp.dp, cp.splits_max, cp.vectors_max, s) != hipSuccess)
+      return XINFER_ERR_LAUNCH;
+    return XINFER_OK;
+  }
   if (launch_decode_capture(c, cp.dp, cp.qr, cp.rounds, cp.decode_blocks, s) != hipSuccess) return XINFER_ERR_LAUNCH;
   if (cp.splits_max > 1) {
     c.total_items = (int32_t)(g.B * g.Hkv * g.T * c.G);

@@ -101,6 +101,18 @@ struct CaptureArgs {
   int64_t blocks_stride;
 };
 
+// Graph-capture prefill: the arguments of a prefill launch and of its merge,
+// planned on the device (prefill.hip: prefill_capture_plan_kernel) from the
+// row counts and lengths in c.offsets, into *attn and *merge, which the
+// prefill and merge kernels of the same graph then read.  Every row goes to
+// the prefill kernel; split_keys comes from the host's plan of the shapes.
+struct PrefillPlanArgs {
+  CaptureArgs c;
+  AttnArgs *attn;
+  MergeArgs *merge;
+  int32_t split_keys;
+};
+
 struct AppendArgs {
   View key, value;
   int64_t key_sd, value_sd;  // feature strides (1 on the vector path)

@@ -22,6 +22,15 @@ hipError_t launch_decode(const AttnArgs &a, int dp, int qr, int rounds, int item
 hipError_t launch_prefill(const AttnArgs &a, int dp, hipStream_t stream);
 // The head-dim-256 prefill kernel over `blocks` blocks (prefill_d256.hip).
 hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t stream);
+// Graph-capture prefill: the plan kernel writes *p.attn and *p.merge from the
+// device offsets, then the prefill kernel runs over `blocks` blocks with its
+// arguments read from *p.attn (blocks past their XCD run exit).
+hipError_t launch_prefill_capture(const PrefillPlanArgs &p, int dp, unsigned blocks, hipStream_t stream);
+hipError_t launch_prefill_d256_dev(const AttnArgs *a, unsigned blocks, hipStream_t stream);
+// The merge with its arguments in device memory (written by the plan
+// kernel): grid for up to max_vectors query vectors; max_splits picks the
+// thread layout.
+hipError_t launch_merge_dev(const MergeArgs *a, int dp, int max_splits, int64_t max_vectors, hipStream_t stream);
 
 // Merges a.total_items query vectors; max_splits picks the thread layout.
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream);

@@ -109,8 +109,11 @@ __device__ __forceinline__ void fold_and_write(MergeRed<FS, SG> &red, const floa
       u32x2{pack_bf16x2(st.o.x * inv, st.o.y * inv), pack_bf16x2(st.o.z * inv, st.o.w * inv)};
 }
 
-template <int DP, int SG, int THREADS, int FS>
-__global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
+// The kernel's body, shared by the launch with host-planned arguments
+// (merge_kernel) and the graph-capture launch that reads them from device
+// memory (merge_dev_kernel).
+template <int DP, int SG, int THREADS, int FS, bool DEV>
+__device__ __forceinline__ void merge_body(const MergeArgs &a) {
   constexpr int FC = DP / 4;                         // feature lanes of a vector
   static_assert(SG == 1 ? FS == FC : FS * SG == THREADS, "block shape");
   constexpr int NS = FC / FS;                        // feature slices per vector (SG > 1)
@@ -136,6 +139,10 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
   // Work groups: VPB vectors (few splits) or one slice of one vector.  The
   // grid is the groups rounded up to a multiple of 8 (launch_merge_d).
   const int groups = SG > 1 ? total_items * NS : (total_items + VPB - 1) / VPB;
+  // A grid sized for more groups (device-planned launches) leaves surplus blocks.
+  if constexpr (DEV) {
+    if ((int)(blockIdx.x / 8) >= (groups + 7) / 8) return;
+  }
   const int group = (int)(blockIdx.x % 8) * ((groups + 7) / 8) + (int)(blockIdx.x / 8);
   const int vec = SG > 1 ? group / NS : group * VPB + vl;
   const int f = SG > 1 ? (group - vec * NS) * FS + fl : fl;  // feature lane of the vector
@@ -175,8 +182,29 @@ __global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
 constexpr int kMergeSliceLanes = 16;
 constexpr int kMergeSliceSplits = 64;
 
-template <int DP>
-static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t stream) {
+template <int DP, int SG, int THREADS, int FS>
+__global__ void __launch_bounds__(THREADS) merge_kernel(const MergeArgs a) {
+  merge_body<DP, SG, THREADS, FS, false>(a);
+}
+
+template <int DP, int SG, int THREADS, int FS>
+__global__ void __launch_bounds__(THREADS) merge_dev_kernel(const MergeArgs *__restrict__ a) {
+  merge_body<DP, SG, THREADS, FS, true>(*a);
+}
+
+// The merge's launch: host arguments `a`, or (DEV) the arguments at `dev`;
+// the grid covers `vectors` query vectors.
+template <int DP, int SG, int THREADS, int FS, bool DEV>
+static void launch_merge_kernel(dim3 grid, const MergeArgs &a, const MergeArgs *dev, hipStream_t stream) {
+  if constexpr (DEV)
+    hipLaunchKernelGGL((merge_dev_kernel<DP, SG, THREADS, FS>), grid, dim3(THREADS), 0, stream, dev);
+  else
+    hipLaunchKernelGGL((merge_kernel<DP, SG, THREADS, FS>), grid, dim3(THREADS), 0, stream, a);
+}
+
+template <int DP, bool DEV>
+static hipError_t launch_merge_d(const MergeArgs &a, const MergeArgs *dev, int max_splits, int64_t vectors,
+                                 hipStream_t stream) {
   constexpr int FC = DP / 4;
   // Grids are rounded up to a multiple of the 8 XCDs; surplus groups exit.
   if (max_splits <= kMergeSerialSplits) {
@@ -185,26 +213,25 @@ static hipError_t launch_merge_d(const MergeArgs &a, int max_splits, hipStream_t
     // 3 us faster than with 4 vectors and half lines; same outputs).
     constexpr int THREADS = DP == 256 ? 512 : 256;
     constexpr int VPB = THREADS / FC;
-    hipLaunchKernelGGL((merge_kernel<DP, 1, THREADS, FC>), dim3(((a.total_items + VPB - 1) / VPB + 7) / 8 * 8),
-                       dim3(THREADS), 0, stream, a);
+    launch_merge_kernel<DP, 1, THREADS, FC, DEV>(dim3(((vectors + VPB - 1) / VPB + 7) / 8 * 8), a, dev, stream);
   } else if (max_splits <= kMergeSliceSplits) {
     // One block per vector, with enough split lanes that each lane loads at
     // most one batch of 16 records when the block can grow to 1024 threads.
-    const dim3 grid((a.total_items + 7) / 8 * 8);
+    const dim3 grid((vectors + 7) / 8 * 8);
     if (max_splits <= 16 * (256 / FC))
-      hipLaunchKernelGGL((merge_kernel<DP, 256 / FC, 256, FC>), grid, dim3(256), 0, stream, a);
+      launch_merge_kernel<DP, 256 / FC, 256, FC, DEV>(grid, a, dev, stream);
     else if (max_splits <= 16 * (512 / FC))
-      hipLaunchKernelGGL((merge_kernel<DP, 512 / FC, 512, FC>), grid, dim3(512), 0, stream, a);
+      launch_merge_kernel<DP, 512 / FC, 512, FC, DEV>(grid, a, dev, stream);
     else
-      hipLaunchKernelGGL((merge_kernel<DP, 1024 / FC, 1024, FC>), grid, dim3(1024), 0, stream, a);
+      launch_merge_kernel<DP, 1024 / FC, 1024, FC, DEV>(grid, a, dev, stream);
   } else {
     // One block per (vector, slice of FS feature lanes).
     constexpr int FS = FC < kMergeSliceLanes ? FC : kMergeSliceLanes;
-    const dim3 grid(((int64_t)a.total_items * (FC / FS) + 7) / 8 * 8);
+    const dim3 grid((vectors * (FC / FS) + 7) / 8 * 8);
     if (max_splits <= 16 * (256 / FS))
-      hipLaunchKernelGGL((merge_kernel<DP, 256 / FS, 256, FS>), grid, dim3(256), 0, stream, a);
+      launch_merge_kernel<DP, 256 / FS, 256, FS, DEV>(grid, a, dev, stream);
     else
-      hipLaunchKernelGGL((merge_kernel<DP, 512 / FS, 512, FS>), grid, dim3(512), 0, stream, a);
+      launch_merge_kernel<DP, 512 / FS, 512, FS, DEV>(grid, a, dev, stream);
   }
   return hipGetLastError();
 }
@@ -260,9 +287,18 @@ hipError_t launch_merge_capture(const CaptureArgs &c, int dp, int max_splits, hi
 
 hipError_t launch_merge(const MergeArgs &a, int dp, int max_splits, hipStream_t stream) {
   switch (dp) {
-    case 64: return launch_merge_d<64>(a, max_splits, stream);
-    case 128: return launch_merge_d<128>(a, max_splits, stream);
-    default: return launch_merge_d<256>(a, max_splits, stream);
+    case 64: return launch_merge_d<64, false>(a, nullptr, max_splits, a.total_items, stream);
+    case 128: return launch_merge_d<128, false>(a, nullptr, max_splits, a.total_items, stream);
+    default: return launch_merge_d<256, false>(a, nullptr, max_splits, a.total_items, stream);
+  }
+}
+
+hipError_t launch_merge_dev(const MergeArgs *a, int dp, int max_splits, int64_t max_vectors, hipStream_t stream) {
+  const MergeArgs none{};
+  switch (dp) {
+    case 64: return launch_merge_d<64, true>(none, a, max_splits, max_vectors, stream);
+    case 128: return launch_merge_d<128, true>(none, a, max_splits, max_vectors, stream);
+    default: return launch_merge_d<256, true>(none, a, max_splits, max_vectors, stream);
   }
 }
 

@@ -78,8 +78,11 @@ struct PrefillShape {
   static constexpr int SMEM = NST * 4 * TILE > FOLD ? NST * 4 * TILE : FOLD;
 };
 
-template <int DP, int KH>
-__global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
+// The kernel's body, shared by the launch with host-planned arguments
+// (prefill_kernel) and the graph-capture launch that reads them from device
+// memory (prefill_dev_kernel).
+template <int DP, int KH, bool DEV>
+__device__ __forceinline__ void prefill_body(const AttnArgs &a) {
   using S = PrefillShape<DP, KH>;
   constexpr int THREADS = S::THREADS, NDS = S::NDS, NDT = S::NDT, CHUNKS = S::CHUNKS;
   constexpr int TILE = S::TILE, LOADS = S::LOADS, NST = S::NST, KPW = S::KPW, NKT = S::NKT;
@@ -124,6 +127,9 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
   const int qrows = cnt * G, p0 = L - cnt;
 
   if (tile == 0 && split == 0 && cnt < T) zero_padded_queries(a, b, h, cnt, G, D, T, tid, THREADS);
+  if constexpr (DEV) {
+    if (cnt == 0) return;  // a row without queries (device-planned launches only): its zeros are written
+  }
 
   // Key range of this tile and split.
   const int j_last = min(tile * kTileQ + kTileQ, qrows) - 1;
@@ -444,6 +450,129 @@ __global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
                                     reinterpret_cast<u32x2 *>(a.part_ml + 2 * (blk + jr)));
     }
   }
+}
+
+template <int DP, int KH>
+__global__ void __launch_bounds__(256 * KH) prefill_kernel(const AttnArgs a) {
+  prefill_body<DP, KH, false>(a);
+}
+
+template <int DP, int KH>
+__global__ void __launch_bounds__(256 * KH) prefill_dev_kernel(const AttnArgs *__restrict__ a) {
+  prefill_body<DP, KH, true>(*a);
+}
+
+// Graph-capture prefill plan: one wave.  Lane r takes row r's count and
+// length from the device offsets (clamped as capture_row does) and its work
+// items as the host planner lays them out -- Hkv x tiles of 128 query vectors
+// x splits of p.split_keys keys, one zero-filling item per kv head for a row
+// without queries -- then the rows' item, record and merge-vector offsets
+// are prefix sums in row order.  The XCD runs cut the items into 8 runs of
+// equal count.  Writes *p.attn and *p.merge with vector stores.
+__global__ void __launch_bounds__(64) prefill_capture_plan_kernel(const PrefillPlanArgs p) {
+  const CaptureArgs &c = p.c;
+  __shared__ int s_items[kMaxRows], s_records[kMaxRows], s_vectors[kMaxRows], s_split[kMaxRows];
+  __shared__ int s_total[3];
+  const int r = threadIdx.x;
+  int count = 0, length = 1, ntiles = 1, nsplit = 1;
+  if (r < c.B) {
+    capture_row(c, r, count, length);
+    if (count > 0) {
+      ntiles = (count * c.G + kTileQ - 1) / kTileQ;
+      nsplit = max(1, (length + p.split_keys - 1) / p.split_keys);
+    }
+    s_items[r] = c.Hkv * ntiles * nsplit;
+    s_records[r] = nsplit > 1 ? c.Hkv * nsplit * ntiles * kTileQ : 0;
+    s_vectors[r] = nsplit > 1 ? c.Hkv * count * c.G : 0;
+    s_split[r] = nsplit > 1;
+  }
+  __syncthreads();
+  if (r == 0) {  // exclusive prefix sums, in place
+    int items = 0, records = 0, vectors = 0, split_rows = 0;
+    for (int k = 0; k < c.B; ++k) {
+      const int ni = s_items[k], nr = s_records[k], nv = s_vectors[k], ns = s_split[k];
+      s_items[k] = items;
+      s_records[k] = records;
+      s_vectors[k] = vectors;
+      s_split[k] = ns ? split_rows : -1;
+      items += ni;
+      records += nr;
+      vectors += nv;
+      split_rows += ns;
+    }
+    s_total[0] = items;
+    s_total[1] = vectors;
+    s_total[2] = split_rows;
+  }
+  __syncthreads();
+  AttnArgs *const a = p.attn;
+  MergeArgs *const m = p.merge;
+  if (r < c.B) {
+    RowSched rs{};
+    rs.batch = r;
+    rs.count = count;
+    rs.length = length;
+    rs.item_begin = s_items[r];
+    rs.nsplit = nsplit;
+    rs.ntiles = ntiles;
+    rs.rec_begin = s_records[r];
+    a->rows[r] = rs;
+    if (s_split[r] >= 0) {
+      MergeRow mr{};
+      mr.batch = r;
+      mr.count = count;
+      mr.nsplit = nsplit;
+      mr.item_begin = s_vectors[r];
+      mr.tiles = ntiles;
+      mr.rec_begin = s_records[r];
+      m->rows[s_split[r]] = mr;
+    }
+  }
+  if (r < 9) a->xcd_begin[r] = (int32_t)((int64_t)r * s_total[0] / 8);
+  if (r == 0) {
+    a->q = c.q;
+    a->k = c.k;
+    a->v = c.v;
+    a->out = c.out;
+    a->o_sb = c.o_sb;
+    a->o_sh = c.o_sh;
+    a->o_st = c.o_st;
+    a->part_o = c.part_o;
+    a->part_ml = c.part_ml;
+    a->scale_log2 = c.scale_log2;
+    a->D = c.D;
+    a->G = c.G;
+    a->Hkv = c.Hkv;
+    a->T = c.T;
+    a->total_items = s_total[0];
+    a->nrows = c.B;
+    a->arrive_ctr = nullptr;
+    a->tag = 0;
+    a->blocks = c.blocks;
+    a->blocks_stride = c.blocks_stride;
+    a->kv_rows = c.B;
+    m->out = c.out;
+    m->o_sb = c.o_sb;
+    m->o_sh = c.o_sh;
+    m->o_st = c.o_st;
+    m->part_o = c.part_o;
+    m->part_ml = c.part_ml;
+    m->D = c.D;
+    m->G = c.G;
+    m->total_items = s_total[1];
+    m->nrows = s_total[2];
+  }
+}
+
+hipError_t launch_prefill_capture(const PrefillPlanArgs &p, int dp, unsigned blocks, hipStream_t stream) {
+  hipLaunchKernelGGL(prefill_capture_plan_kernel, dim3(1), dim3(64), 0, stream, p);
+  if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
+  switch (dp) {
+    case 64: hipLaunchKernelGGL((prefill_dev_kernel<64, 2>), dim3(blocks), dim3(512), 0, stream, p.attn); break;
+    case 128: hipLaunchKernelGGL((prefill_dev_kernel<128, 2>), dim3(blocks), dim3(512), 0, stream, p.attn); break;
+    default: return launch_prefill_d256_dev(p.attn, blocks, stream);
+  }
+  return hipGetLastError();
 }
 
 // Blocks per launch: 8 times the longest XCD run (blocks past their run exit

@@ -60,7 +60,10 @@ static_assert(kLoads * kThreads == kBN * kChunks, "tile = whole load instruction
 static_assert(kSmemBytes <= 160 * 1024, "LDS");
 }  // namespace
 
-__global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a) {
+// The kernel's body, shared by the launch with host-planned arguments and
+// the graph-capture launch that reads them from device memory.
+template <bool DEV>
+__device__ __forceinline__ void prefill_d256_body(const AttnArgs &a) {
   __shared__ __attribute__((aligned(16))) uint16_t smem[kSmemBytes / 2];
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
@@ -96,6 +99,9 @@ __global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a
   const int qrows = cnt * G, p0 = L - cnt;
 
   if (tile == 0 && split == 0 && cnt < T) zero_padded_queries(a, b, h, cnt, G, D, T, tid, kThreads);
+  if constexpr (DEV) {
+    if (cnt == 0) return;  // a row without queries (device-planned launches only): its zeros are written
+  }
 
   // Key range of this tile and split.
   const int j_last = min(tile * kTileQ + kTileQ, qrows) - 1;
@@ -369,8 +375,19 @@ __global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a
   }
 }
 
+__global__ void __launch_bounds__(kThreads) prefill_d256_kernel(const AttnArgs a) { prefill_d256_body<false>(a); }
+
+__global__ void __launch_bounds__(kThreads) prefill_d256_dev_kernel(const AttnArgs *__restrict__ a) {
+  prefill_d256_body<true>(*a);
+}
+
 hipError_t launch_prefill_d256(const AttnArgs &a, unsigned blocks, hipStream_t stream) {
   hipLaunchKernelGGL(prefill_d256_kernel, dim3(blocks), dim3(kThreads), 0, stream, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_prefill_d256_dev(const AttnArgs *a, unsigned blocks, hipStream_t stream) {
+  hipLaunchKernelGGL(prefill_d256_dev_kernel, dim3(blocks), dim3(kThreads), 0, stream, a);
   return hipGetLastError();
 }
 
