@@ -129,7 +129,7 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
  * writes into the workspace from device_offsets at run time (the split length
  * is chosen on the host for rows of T queries over C keys).  B <= 64
  * (XINFER_ERR_CAPTURE_ROWS otherwise).  Device lengths are not validated on
- * the host: counts are clamped to [0, T] and lengths to [max(count, 1), C], so
+ * the host: counts are clamped to [0, min(T, C)] and lengths to [max(count, 1), C], so
  * bad values give wrong rows but never an access outside the tensors.
  * Results agree with xinfer_batched_flash_attention within rounding; the
  * kernels are the same, but every launch covers the capacity. */

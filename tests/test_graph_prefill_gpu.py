@@ -1,23 +1,25 @@
 """A prefill (chunked) step captured once in a HIP graph and replayed while the lengths change.
 
 For shapes with more than 8 query vectors per KV head (T * Hq/Hkv > 8),
-xinfer::batched_flash_attention_graph plans on the device: a one-wave plan
-kernel reads every row's query count and KV length from cuda_offsets and
-writes the prefill kernel's and the merge kernel's arguments into the
-workspace (prefill.hip: prefill_capture_plan_kernel), with the split size the
-host planner gives the shapes at capacity; the prefill and merge kernels then
-read their arguments from there, over grids sized for every row at capacity
-(blocks past the planned items exit).  Every row takes the prefill kernel,
-including rows with one query and rows without queries (which only zero
-their outputs).
+xinfer::batched_flash_attention_graph plans on the device: a plan kernel
+reads every row's query count and KV length from cuda_offsets, picks the key
+split size for those lengths, cuts the items into XCD runs of about equal
+work, and writes the prefill kernel's and the merge kernel's arguments into
+the workspace (prefill.hip: prefill_capture_plan_kernel); the prefill and
+merge kernels then read their arguments from there, over grids sized for the
+most items the plan can make (blocks past the planned items exit).  Every row
+takes the prefill kernel, including rows with one query and rows without
+queries (which only zero their outputs).
 
 As for decode (tests/test_graph_decode_gpu.py): the append and the attention
 are captured once, and every replay over the length sets below must equal,
 bit for bit, the same operators launched eagerly, stay within the float64
 oracle's gates, and agree with the default operator (host-planned, other
 splits) within the same gates.  Shapes: Qwen3 chunks (G = 2, two query tiles
-per row, split rows merged), Qwen3.5 chunks (D = 256, G = 4), head dim 64
-with G = 1 (one tile), and a capacity that needs no split (no merge launch).
+per row, split rows merged), Qwen3.5 chunks (D = 256, G = 4), eight ragged
+Qwen3.5 rows (split and unsplit rows in one launch, cuts inside rows), head
+dim 64 with G = 1 (one tile), and a capacity that needs no split (no merge
+launch).
 """
 
 import pytest
@@ -37,6 +39,10 @@ SHAPES = {
     "qwen35_chunks": (16, 4, 256, 64, 2048, [
         [(64, 2048), (1, 77), (33, 1500), (0, 3)],
         [(64, 64), (64, 2000), (2, 2), (64, 1024)],
+    ]),
+    "qwen35_ragged8": (16, 4, 256, 96, 8192, [
+        [(96, 8000), (40, 1200), (96, 3000), (3, 6000), (96, 96), (0, 5), (70, 7000), (1, 1)],
+        [(96, 8192), (96, 8100), (1, 4000), (96, 500), (50, 50), (96, 2600), (0, 1), (17, 5000)],
     ]),
     "d64_group1": (8, 8, 64, 40, 1024, [
         [(40, 1024), (5, 500), (40, 40), (1, 1)],

@@ -230,11 +230,14 @@ def test_noalloc_rejects_plans_beyond_its_scratch_before_any_launch(lib):
 
 def test_graph_mode_shapes_and_workspace(lib):
     """The graph-capture entry point plans from shapes alone: its workspace
-    holds every row's records at capacity, and rows that would take the
-    prefill kernel (T * Hq/Hkv > 8) or more than 64 rows are refused before
-    any launch.  Items take four rounds of 128 keys (D = 128, two query
-    vectors per KV head) when the capacity layout holds at least 1536
-    one-round items and at most 2048 four-round ones, else one round."""
+    holds every row's records at capacity, and more than 64 rows are refused
+    before any launch.  Decode items take four rounds of 128 keys (D = 128,
+    two query vectors per KV head) when the capacity layout holds at least
+    1536 one-round items and at most 2048 four-round ones, else one round.
+    Prefill shapes (T * Hq/Hkv > 8) hold records for the most items the
+    device plan can lay out: 2048 plus one per (row, kv head, query tile), or
+    every such unit split 8 ways (C / 512 ways below 4096 keys), whichever
+    is fewer, followed by the device-written prefill and merge arguments."""
     lib.xinfer_batched_flash_attention_graph_workspace_size.restype = ctypes.c_size_t
 
     def workspace(batch, capacity):
@@ -249,6 +252,20 @@ def test_graph_mode_shapes_and_workspace(lib):
     assert workspace(1, 4096) == records_bytes(1, 4096 // 128)     # 256 one-round items
     assert workspace(16, 16384) == records_bytes(16, 16384 // 128)  # 4096 four-round items: one round
     assert lib.xinfer_status_string(18).decode() == "Graph-capture attention takes at most 64 rows"
+
+    def prefill_workspace(batch, tokens, capacity, hq=16, hkv=8, dim=128):
+        q, k = view([batch, hq, tokens, dim]), view([batch, hkv, capacity, dim])
+        return lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(q), ctypes.byref(k))
+
+    def prefill_records_bytes(units, splits, dim=128):
+        records = min(2048 + units, units * splits) * 128
+        return -(-records * dim * 4 // 256) * 256 + records * 8
+
+    for (batch, tokens, capacity, splits) in [(4, 128, 4096, 8), (8, 512, 16384, 8), (2, 64, 1024, 2)]:
+        units = batch * 8 * -(-tokens * 2 // 128)
+        size, records = prefill_workspace(batch, tokens, capacity), prefill_records_bytes(units, splits)
+        assert records < size < records + 8192, (batch, tokens, capacity)
+    assert prefill_workspace(2, 64, 512) < 8192  # 512 keys: never split, no records
 
     def graph(qv, kv):
         return lib.xinfer_batched_flash_attention_graph(ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv),

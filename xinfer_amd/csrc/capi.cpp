@@ -661,7 +661,7 @@ struct CapturePlan {
   // planned on the device; the workspace also holds the prefill and merge
   // arguments the plan kernel writes.
   bool prefill = false;
-  int64_t split_keys = 0, items_max = 0, vectors_max = 0;
+  int64_t items_max = 0, vectors_max = 0;
   size_t part_ml_offset() const { return (size_t)((records * dp_d * 4 + 255) / 256 * 256); }
   size_t records_bytes() const { return records ? part_ml_offset() + (size_t)records * 8 : 0; }
   size_t attn_offset() const { return (records_bytes() + 255) / 256 * 256; }
@@ -690,16 +690,22 @@ int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
   cp.dp = padded_dim(g.D);
   cp.dp_d = g.D;
   if (g.T * G > kDecodeMaxQueryVectors) {
-    // Prefill shapes: the split size of the host plan with every row at T
-    // queries and C keys; the device plan gives each row at most
-    // tiles x splits items of that size.
+    // Prefill shapes: the device plan (prefill.hip:
+    // prefill_capture_plan_kernel) picks the split size from the lengths, in
+    // the range choose_split_keys searches, so that the items stay below
+    // 2048 + one per (row, kv head, query tile); no row takes more than
+    // kMergeSerialSplits splits (or splits below kPrefillMinSplitKeys keys).
+    // The prefill grid, the records and the merge grid are sized for that.
     cp.prefill = true;
-    const std::vector<int32_t> counts((size_t)g.B, (int32_t)g.T), lengths((size_t)g.B, (int32_t)g.C);
-    cp.split_keys = choose_split_keys(g, counts, lengths, (int)G, cp.dp);
-    cp.splits_max = prefill_splits(g.C, cp.split_keys);
-    cp.items_max = g.B * g.Hkv * ceil_div(g.T * G, kPrefillTileQ) * cp.splits_max;
+    const int64_t unsplit = g.B * g.Hkv * ceil_div(g.T * G, kPrefillTileQ);
+    cp.splits_max = (int)std::min<int64_t>(kMergeSerialSplits, ceil_div(g.C, kPrefillMinSplitKeys));
+    cp.items_max = std::min(2048 + unsplit, unsplit * cp.splits_max);
     cp.vectors_max = g.B * g.Hkv * g.T * G;
     cp.records = cp.splits_max > 1 ? cp.items_max * kPrefillTileQ : 0;
+    // Item, record and vector indices are 32-bit on the device (a q tensor
+    // that large would not fit in memory).
+    if (cp.items_max * kPrefillTileQ >= (int64_t(1) << 31) || cp.vectors_max >= (int64_t(1) << 31))
+      return XINFER_ERR_QKV_SHAPES;
     return XINFER_OK;
   }
   cp.qr = pow2_at_least((int)std::max<int64_t>(1, g.T * G));
@@ -838,11 +844,16 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
     pp.c = c;
     pp.attn = reinterpret_cast<AttnArgs *>(ws + cp.attn_offset());
     pp.merge = reinterpret_cast<MergeArgs *>(ws + cp.merge_offset());
-    pp.split_keys = (int32_t)cp.split_keys;
-    // Equal-count XCD runs of at most items_max items: 8 runs of at most
-    // ceil(items_max / 8) blocks each.
-    const unsigned blocks8 = (unsigned)(8 * ceil_div(cp.items_max, 8));
-    if (launch_prefill_capture(pp, cp.dp, blocks8, s) != hipSuccess) return XINFER_ERR_LAUNCH;
+    pp.items_max = (int32_t)cp.items_max;
+    // 8 XCD runs of at most ceil(items_max / 8) items (the plan clamps its cuts).
+    pp.run_max = (int32_t)ceil_div(cp.items_max, 8);
+    pp.splits_max = cp.splits_max;
+    pp.min_split_keys = (int32_t)kPrefillMinSplitKeys;
+    pp.tile_us = (float)prefill_tile_us(cp.dp);
+    pp.item_us = (float)kPrefillItemUs;
+    pp.merge_us = (float)kMergeLaunchUs;
+    pp.record_us = (float)(2.0 * (cp.dp * 4 + 8) / kRecordBytesPerUs);
+    if (launch_prefill_capture(pp, cp.dp, (unsigned)(8 * pp.run_max), s) != hipSuccess) return XINFER_ERR_LAUNCH;
     if (cp.splits_max > 1 && launch_merge_dev(pp.merge, cp.dp, cp.splits_max, cp.vectors_max, s) != hipSuccess)
       return XINFER_ERR_LAUNCH;
     return XINFER_OK;

@@ -253,7 +253,7 @@ __device__ __forceinline__ int page_in_range(int page, int rows) { return min(ma
 // ranges the host validates in the default mode (see CaptureArgs in kernel_args.h).
 __device__ __forceinline__ void capture_row(const CaptureArgs &c, int r, int &count, int &length) {
   const int32_t *cuq = c.offsets, *cuk = c.offsets + c.B + 1;
-  count = min(max(cuq[r + 1] - cuq[r], 0), c.T);
+  count = min(max(cuq[r + 1] - cuq[r], 0), min(c.T, c.C));
   length = min(max(cuk[r + 1] - cuk[r], max(count, 1)), c.C);
 }
 

@@ -84,7 +84,7 @@ struct MergeArgs {
 // the device copy of the cumulative offsets instead of a host schedule.
 // Records are laid out per row at capacity: row r's start at r * row_records,
 // in the decode layout [kv head][split][vector] with the row's actual split
-// count.  Counts are clamped to [0, T] and lengths to [max(count, 1), C], so
+// count.  Counts are clamped to [0, min(T, C)] and lengths to [max(count, 1), C], so
 // no device data can address outside q, k, v, out or the workspace.
 struct CaptureArgs {
   View q, k, v;
@@ -105,12 +105,20 @@ struct CaptureArgs {
 // planned on the device (prefill.hip: prefill_capture_plan_kernel) from the
 // row counts and lengths in c.offsets, into *attn and *merge, which the
 // prefill and merge kernels of the same graph then read.  Every row goes to
-// the prefill kernel; split_keys comes from the host's plan of the shapes.
+// the prefill kernel.  The limits are those the host sized the grids and the
+// records for; the costs are the host planner's model (capi.cpp).
 struct PrefillPlanArgs {
   CaptureArgs c;
   AttnArgs *attn;
   MergeArgs *merge;
-  int32_t split_keys;
+  int32_t items_max;       // work items the records hold; the plan never exceeds it
+  int32_t run_max;         // blocks per XCD of the prefill grid (8 * run_max blocks)
+  int32_t splits_max;      // key splits a row may take (<= kMergeSerialSplits)
+  int32_t min_split_keys;  // smallest split
+  float tile_us;           // one 64-key tile of one item
+  float item_us;           // fixed cost of an item
+  float merge_us;          // the merge launch, when any row splits
+  float record_us;         // one record (one query vector of one split) written and read
 };
 
 struct AppendArgs {

@@ -462,74 +462,228 @@ __global__ void __launch_bounds__(256 * KH) prefill_dev_kernel(const AttnArgs *_
   prefill_body<DP, KH, true>(*a);
 }
 
-// Graph-capture prefill plan: one wave.  Lane r takes row r's count and
-// length from the device offsets (clamped as capture_row does) and its work
-// items as the host planner lays them out -- Hkv x tiles of 128 query vectors
-// x splits of p.split_keys keys, one zero-filling item per kv head for a row
-// without queries -- then the rows' item, record and merge-vector offsets
-// are prefix sums in row order.  The XCD runs cut the items into 8 runs of
-// equal count.  Writes *p.attn and *p.merge with vector stores.
-__global__ void __launch_bounds__(64) prefill_capture_plan_kernel(const PrefillPlanArgs p) {
+// ceil(a / b) for 0 <= a, 0 < b < 2^31.
+__device__ __forceinline__ int plan_ceil_div(int a, int b) {
+  return (int)(((unsigned)a + (unsigned)b - 1u) / (unsigned)b);
+}
+
+// Inclusive prefix over the 64 lanes of the wave, in a fixed order.
+template <typename V>
+__device__ __forceinline__ V wave_inclusive_scan(V x, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d *= 2) {
+    const V y = __shfl_up(x, d, 64);
+    if (lane >= d) x += y;
+  }
+  return x;
+}
+
+__device__ __forceinline__ int read_lane(int x, int lane) { return __builtin_amdgcn_readlane(x, lane); }
+__device__ __forceinline__ float read_lane(float x, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), lane));
+}
+
+constexpr int kPlanCandidates = kMaxRows * kMergeSerialSplits + 2;
+constexpr int kPlanThreads = 1024;
+
+// Graph-capture prefill plan: one block; its first wave holds one row per
+// lane (B <= 64).
+//  1. Lane r takes row r's count and length (capture_row) and its tiles of
+//     128 query vectors, and estimates the 64-key tiles that all its tiles'
+//     causal key ranges hold (a tile's splits together read its range once,
+//     whatever the split size): tile t ends near key p0 + (t + 1) * 128 / G,
+//     the last at the row's length, plus half a tile each for the partial
+//     last 64 keys.
+//  2. The split size.  Candidates are the host planner's range -- 256 to 2048
+//     items' worth of keys, at least min_split_keys -- raised so that no row
+//     takes more than splits_max splits, and within it every row's
+//     split-count change points.  Each is priced, by a group of lanes with a
+//     lane per row, as the larger of (work over 256 CUs + 3/4 of the longest
+//     item) and the longest item, plus the records' trips and the merge
+//     launch when a row splits, in the host planner's cost model (between the
+//     list-scheduling bounds, where the host simulates the dispatch).  The
+//     cheapest wins; ties go to the larger.
+//  3. Rows' item, record and merge-vector offsets are wave prefix sums.  A
+//     plan over items_max items (the limits make that impossible) would fall
+//     back to unsplit rows, which always fit.
+//  4. XCD runs of about equal work, as the host cuts them, with the cut inside
+//     a (row, kv head) placed in proportion to its items, then clamped so that
+//     no run exceeds run_max items.
+// Writes *p.attn and *p.merge.
+__global__ void __launch_bounds__(kPlanThreads) prefill_capture_plan_kernel(const PrefillPlanArgs p) {
   const CaptureArgs &c = p.c;
-  __shared__ int s_items[kMaxRows], s_records[kMaxRows], s_vectors[kMaxRows], s_split[kMaxRows];
-  __shared__ int s_total[3];
-  const int r = threadIdx.x;
-  int count = 0, length = 1, ntiles = 1, nsplit = 1;
-  if (r < c.B) {
-    capture_row(c, r, count, length);
-    if (count > 0) {
-      ntiles = (count * c.G + kTileQ - 1) / kTileQ;
-      nsplit = max(1, (length + p.split_keys - 1) / p.split_keys);
+  __shared__ int4 s_row[kMaxRows];  // count, length, query tiles, key tiles (float bits)
+  __shared__ int s_cand[kPlanCandidates];
+  __shared__ int s_ncand;
+  __shared__ unsigned long long s_best;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int B = c.B, G = c.G, Hkv = c.Hkv;
+  const bool row_lane = tid < 64 && lane < B;
+  int count = 0, length = 1, ntiles = 1;
+  float kvtiles = 0.f;
+  if (tid < 64) {
+    if (row_lane) {
+      capture_row(c, lane, count, length);
+      if (count > 0) {
+        ntiles = (count * G + kTileQ - 1) / kTileQ;
+        const float m = (float)(ntiles - 1);
+        kvtiles = (m * (float)(length - count) + (float)kTileQ / (float)G * m * (m + 1.f) * 0.5f + (float)length) *
+                      (1.f / 64.f) + 0.5f * (float)ntiles;
+      }
+      s_row[lane] = make_int4(count, length, ntiles, __float_as_int(kvtiles));
     }
-    s_items[r] = c.Hkv * ntiles * nsplit;
-    s_records[r] = nsplit > 1 ? c.Hkv * nsplit * ntiles * kTileQ : 0;
-    s_vectors[r] = nsplit > 1 ? c.Hkv * count * c.G : 0;
-    s_split[r] = nsplit > 1;
+    // Keys of the rows with queries (host: choose_split_keys) and the longest row.
+    int64_t keys = count > 0 ? (int64_t)Hkv * ntiles * length : 0;
+    int longest_row = count > 0 ? length : 1;
+#pragma unroll
+    for (int d = 32; d >= 1; d /= 2) {
+      keys += __shfl_xor(keys, d, 64);
+      longest_row = max(longest_row, __shfl_xor(longest_row, d, 64));
+    }
+    auto keys_for = [&](int64_t target) {
+      return max((int64_t)p.min_split_keys, ((keys + target - 1) / target + 63) / 64 * 64);
+    };
+    const int64_t floor_keys = (int64_t)plan_ceil_div(plan_ceil_div(longest_row, p.splits_max), 64) * 64;
+    const int64_t lo64 = max(keys_for(2048), floor_keys), hi64 = max(keys_for(256), lo64);
+    const int lo = (int)min<int64_t>(lo64, 0x7fffffff), hi = (int)min<int64_t>(hi64, 0x7fffffff);
+    // Row lane r's change points: the smallest split (a multiple of 64) that
+    // cuts it into n splits, for every n the range allows (n <= splits_max),
+    // listed without gaps after those of the rows before it.
+    int n = 1, n1 = 0;
+    if (row_lane && count > 0) {
+      n = max(1, plan_ceil_div(length, hi));
+      n1 = min(plan_ceil_div(length, lo), p.splits_max);
+    }
+    int mine[kMergeSerialSplits], found = 0;
+#pragma unroll
+    for (int i = 0; i < kMergeSerialSplits; ++i, ++n) {
+      const int k = n <= n1 ? max(p.min_split_keys, plan_ceil_div(plan_ceil_div(length, n), 64) * 64) : 0;
+      mine[i] = k >= lo && k <= hi ? k : 0;
+      found += mine[i] > 0;
+    }
+    const int listed = wave_inclusive_scan(found, lane);
+    int at = 2 + listed - found;
+#pragma unroll
+    for (int i = 0; i < kMergeSerialSplits; ++i)
+      if (mine[i] > 0) s_cand[at++] = mine[i];
+    if (tid == 0) {
+      s_cand[0] = lo;
+      s_cand[1] = hi;
+      s_ncand = 2 + read_lane(listed, 63);
+      s_best = ~0ull;
+    }
   }
   __syncthreads();
-  if (r == 0) {  // exclusive prefix sums, in place
-    int items = 0, records = 0, vectors = 0, split_rows = 0;
-    for (int k = 0; k < c.B; ++k) {
-      const int ni = s_items[k], nr = s_records[k], nv = s_vectors[k], ns = s_split[k];
-      s_items[k] = items;
-      s_records[k] = records;
-      s_vectors[k] = vectors;
-      s_split[k] = ns ? split_rows : -1;
-      items += ni;
-      records += nr;
-      vectors += nv;
-      split_rows += ns;
+  // Thread t prices candidate t / R over row t % R, R the power of two at or
+  // above B; the R lanes of a candidate then sum its work and records and
+  // take its longest item.
+  const int group = B <= 1 ? 1 : 1 << (32 - __clz(B - 1));
+  const int ncand = s_ncand, per_pass = kPlanThreads / group;
+  for (int base = 0; base < ncand; base += per_pass) {
+    const int ci = base + tid / group, r = tid % group;
+    const int k = ci < ncand ? s_cand[ci] : 0;
+    float work = 0.f, longest = 0.f;
+    int64_t records = 0;
+    if (k > 0 && r < B) {
+      const int4 row = s_row[r];
+      if (row.x == 0) {
+        work = (float)Hkv * p.item_us;
+        longest = p.item_us;
+      } else {
+        const int L = row.y, nt = row.z;
+        const int ns = plan_ceil_div(L, k);
+        const int per = plan_ceil_div(plan_ceil_div(L, ns), 64) * 64;
+        work = (float)Hkv * (__int_as_float(row.w) * p.tile_us + (float)(ns * nt) * p.item_us);
+        longest = (float)plan_ceil_div(min(per, L), 64) * p.tile_us + p.item_us;
+        records = ns > 1 ? (int64_t)Hkv * ns * nt * kTileQ : 0;
+      }
     }
-    s_total[0] = items;
-    s_total[1] = vectors;
-    s_total[2] = split_rows;
+    for (int d = 1; d < group; d *= 2) {
+      work += __shfl_xor(work, d, 64);
+      longest = fmaxf(longest, __shfl_xor(longest, d, 64));
+      records += __shfl_xor(records, d, 64);
+    }
+    if (k > 0 && r == 0) {
+      const float us = fmaxf(work * (1.f / 256.f) + 0.75f * longest, longest) +
+                       (records ? p.merge_us + (float)records * p.record_us : 0.f);
+      atomicMin(&s_best, ((unsigned long long)__float_as_uint(us) << 32) | (unsigned)(0x7fffffff - k));
+    }
   }
   __syncthreads();
+  if (tid >= 64) return;
+  const int split_keys = s_best == ~0ull ? 0x7fffffff : 0x7fffffff - (int)(uint32_t)s_best;
+  int nsplit = count > 0 ? plan_ceil_div(length, split_keys) : 1;
+  int items = row_lane ? Hkv * ntiles * nsplit : 0;
+  int all_items = items;
+#pragma unroll
+  for (int d = 32; d >= 1; d /= 2) all_items += __shfl_xor(all_items, d, 64);
+  if (all_items > p.items_max) {  // unreachable with the host's limits; unsplit rows fit
+    nsplit = 1;
+    items = row_lane ? Hkv * ntiles : 0;
+  }
+  const bool split = row_lane && nsplit > 1;
+  const int records = split ? Hkv * nsplit * ntiles * kTileQ : 0;
+  const int vectors = split ? Hkv * count * G : 0;
+  const float work = row_lane ? (float)Hkv * (kvtiles * p.tile_us + (float)(nsplit * ntiles) * p.item_us) : 0.f;
+  const int item_end = wave_inclusive_scan(items, lane), rec_end = wave_inclusive_scan(records, lane),
+            vec_end = wave_inclusive_scan(vectors, lane), split_end = wave_inclusive_scan((int)split, lane);
+  const float work_end = wave_inclusive_scan(work, lane);
+  const int item_begin = item_end - items, rec_begin = rec_end - records;
+  // Taken from the previous lane, so that the rows' work ranges tile exactly.
+  const float work_before = __shfl_up(work_end, 1, 64), work_begin = lane == 0 ? 0.f : work_before;
+  const int total_items = read_lane(item_end, 63), total_vectors = read_lane(vec_end, 63),
+            split_rows = read_lane(split_end, 63);
+  const float total_work = read_lane(work_end, 63);
   AttnArgs *const a = p.attn;
   MergeArgs *const m = p.merge;
-  if (r < c.B) {
+  if (row_lane) {
     RowSched rs{};
-    rs.batch = r;
+    rs.batch = lane;
     rs.count = count;
     rs.length = length;
-    rs.item_begin = s_items[r];
+    rs.item_begin = item_begin;
     rs.nsplit = nsplit;
     rs.ntiles = ntiles;
-    rs.rec_begin = s_records[r];
-    a->rows[r] = rs;
-    if (s_split[r] >= 0) {
+    rs.rec_begin = rec_begin;
+    a->rows[lane] = rs;
+    if (split) {
       MergeRow mr{};
-      mr.batch = r;
+      mr.batch = lane;
       mr.count = count;
       mr.nsplit = nsplit;
-      mr.item_begin = s_vectors[r];
+      mr.item_begin = vec_end - vectors;
       mr.tiles = ntiles;
-      mr.rec_begin = s_records[r];
-      m->rows[s_split[r]] = mr;
+      mr.rec_begin = rec_begin;
+      m->rows[split_end - 1] = mr;
     }
   }
-  if (r < 9) a->xcd_begin[r] = (int32_t)((int64_t)r * s_total[0] / 8);
-  if (r == 0) {
+  // XCD runs: cut x at x/8 of the work, inside the (row, kv head) that holds
+  // it -- every lane places the cuts that fall in its row, then each cut is
+  // read from the lane that holds it.
+  int cut[9];
+  cut[0] = 0;
+  cut[8] = total_items;
+#pragma unroll
+  for (int x = 1; x < 8; ++x) {
+    const float target = total_work * (float)x * 0.125f;
+    const bool in = row_lane && work > 0.f && work_begin <= target && target < work_end;
+    int mine = 0;
+    if (in) {
+      const int per_head = ntiles * nsplit;
+      const float rel = (target - work_begin) / (work / (float)Hkv);
+      const int h = min((int)rel, Hkv - 1);
+      const int within = min((int)((rel - (float)h) * (float)per_head + 0.5f), per_head);
+      mine = min(item_begin + h * per_head + within, total_items);
+    }
+    const unsigned long long holders = __ballot(in);
+    cut[x] = holders ? read_lane(mine, __ffsll((long long)holders) - 1) : total_items;
+  }
+#pragma unroll
+  for (int x = 1; x < 8; ++x)
+    cut[x] = min(max(cut[x], max(cut[x - 1], total_items - (8 - x) * p.run_max)), cut[x - 1] + p.run_max);
+  if (tid == 0) {
+#pragma unroll
+    for (int x = 0; x < 9; ++x) a->xcd_begin[x] = cut[x];
     a->q = c.q;
     a->k = c.k;
     a->v = c.v;
@@ -544,7 +698,7 @@ __global__ void __launch_bounds__(64) prefill_capture_plan_kernel(const PrefillP
     a->G = c.G;
     a->Hkv = c.Hkv;
     a->T = c.T;
-    a->total_items = s_total[0];
+    a->total_items = total_items;
     a->nrows = c.B;
     a->arrive_ctr = nullptr;
     a->tag = 0;
@@ -559,13 +713,13 @@ __global__ void __launch_bounds__(64) prefill_capture_plan_kernel(const PrefillP
     m->part_ml = c.part_ml;
     m->D = c.D;
     m->G = c.G;
-    m->total_items = s_total[1];
-    m->nrows = s_total[2];
+    m->total_items = total_vectors;
+    m->nrows = split_rows;
   }
 }
 
 hipError_t launch_prefill_capture(const PrefillPlanArgs &p, int dp, unsigned blocks, hipStream_t stream) {
-  hipLaunchKernelGGL(prefill_capture_plan_kernel, dim3(1), dim3(64), 0, stream, p);
+  hipLaunchKernelGGL(prefill_capture_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
   if (hipError_t err = hipGetLastError(); err != hipSuccess) return err;
   switch (dp) {
     case 64: hipLaunchKernelGGL((prefill_dev_kernel<64, 2>), dim3(blocks), dim3(512), 0, stream, p.attn); break;
