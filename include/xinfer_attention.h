@@ -125,10 +125,10 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
  * (and the page table, read the same way).
  * The workspace size depends on the shapes only (all rows at capacity C).
  * Shapes with T * (Hq/Hkv) <= 8 take the decode kernels; larger ones take the
- * prefill kernels, whose work list and key splits a one-wave plan kernel
- * writes into the workspace from device_offsets at run time (the split length
- * is chosen on the host for rows of T queries over C keys).  B <= 64
- * (XINFER_ERR_CAPTURE_ROWS otherwise).  Device lengths are not validated on
+ * prefill kernels, whose key split size, work list and XCD runs a plan kernel
+ * chooses from device_offsets at run time and writes into the workspace (at
+ * most 8 splits a row; the workspace holds records for the most items such a
+ * plan can make).  B <= 64 (XINFER_ERR_CAPTURE_ROWS otherwise).  Device lengths are not validated on
  * the host: counts are clamped to [0, min(T, C)] and lengths to [max(count, 1), C], so
  * bad values give wrong rows but never an access outside the tensors.
  * Results agree with xinfer_batched_flash_attention within rounding; the

@@ -16,8 +16,8 @@ permutation, a repeating table, entries out of [0, B) (clamped into it), and
 a table viewed with a row stride of 2.  Paths: one-round and four-round
 decode, decode rows merged inside the decode launch, prefill at head dims
 128 and 256 with and without key splits, head dim 64, the [B, T, Hq, D]
-output and the capture-once decode operator.  A capacity that is not a
-multiple of 256 ignores the table.
+output and the capture-once operator (decode and prefill shapes).  A
+capacity that is not a multiple of 256 ignores the table.
 """
 
 import numpy as np
@@ -121,18 +121,28 @@ def test_page_table_reads_the_named_rows(gpu_ops, name, heads, kv_heads, dim, co
             assert errors["relative_l2"] < 0.01 and errors["peak_relative"] <= 0.05, (name, table, r, errors)
 
 
+# (name, Hq, Hkv, D, counts, lengths, capacity) of the capture-once operator:
+# decode kernels, and the device-planned prefill kernels (split and unsplit rows).
+CAPTURE_CASES = (
+    ("capture_decode", 16, 8, 128, [1, 1, 1, 0], [700, 1500, 33, 9], 2048),
+    ("capture_prefill_dim128", 16, 8, 128, [100, 1, 64, 0], [2000, 33, 64, 9], 2048),
+    ("capture_prefill_dim256", 16, 4, 256, [60, 130, 7], [1500, 1300, 7], 1536),
+)
+
+
+@pytest.mark.parametrize("name,heads,kv_heads,dim,counts,lengths,capacity", CAPTURE_CASES,
+                         ids=[c[0] for c in CAPTURE_CASES])
 @torch.inference_mode()
-def test_capture_operator_reads_the_named_rows(gpu_ops):
-    """The capture-once decode operator reads the table on the device too."""
-    counts, lengths, capacity = [1, 1, 1, 0], [700, 1500, 33, 9], 2048
+def test_capture_operator_reads_the_named_rows(gpu_ops, name, heads, kv_heads, dim, counts, lengths, capacity):
+    """The capture-once operator reads the table on the device too."""
     host, cu, identity = batched_attention_metadata(
         torch.tensor(lengths, dtype=torch.int32), torch.tensor(counts, dtype=torch.int32), "cuda")
     for table, entries, pages in tables(len(counts)):
-        log(f"capture-once decode, page table {table}: pages={pages}")
-        q, k, v = make_inputs("capture", 16, 8, 128, counts, lengths, capacity, pages)
-        out = gpu_ops.batched_flash_attention_graph(q, k, v, host, cu, device_table(entries), 128 ** -0.5)
+        log(f"{name}, page table {table}: counts={counts} lengths={lengths} pages={pages}")
+        q, k, v = make_inputs(name, heads, kv_heads, dim, counts, lengths, capacity, pages)
+        out = gpu_ops.batched_flash_attention_graph(q, k, v, host, cu, device_table(entries), dim ** -0.5)
         expected = gpu_ops.batched_flash_attention_graph(q, k[pages].contiguous(), v[pages].contiguous(), host, cu,
-                                                         identity, 128 ** -0.5)
+                                                         identity, dim ** -0.5)
         torch.cuda.synchronize()
         assert torch.equal(bits(out), bits(expected)), table
         assert not bool(torch.isnan(out.float()).any()), table

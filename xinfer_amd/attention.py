@@ -12,9 +12,10 @@ which registers these operators in the `xinfer` namespace:
   reference's Triton op (compiler/common/kernels/kv_cache.py:45-72);
 * ``batched_flash_attention_bthd`` -- ``batched_flash_attention`` with its
   output in [B,T,Hq,D] order (the adapter's reshape then needs no copy);
-* ``batched_flash_attention_graph`` -- ``batched_flash_attention`` for decode
-  batches that are captured once in a HIP graph and replayed while the
-  lengths change: the kernels read the lengths from ``cuda_offsets``;
+* ``batched_flash_attention_graph`` -- ``batched_flash_attention`` for steps
+  that are captured once in a HIP graph and replayed while the lengths
+  change: the kernels read the lengths from ``cuda_offsets`` (prefill shapes
+  are planned by a kernel from them);
 * ``projection_gemv`` -- the decoder's singleton projections, native instead
   of the reference's Triton op (compiler/common/kernels/projection_gemv.py);
 * ``qk_norm_rope_append`` -- the step before the attention operator in one

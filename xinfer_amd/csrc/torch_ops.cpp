@@ -138,8 +138,9 @@ at::Tensor batched_flash_attention_bthd(const at::Tensor &q, const at::Tensor &k
   return batched_attention(q, k, v, offsets, cuda_offsets, blocks, scale, true);
 }
 
-// Graph-capture variant of batched_flash_attention (decode batches): the same
-// schema, but the row lengths come from cuda_offsets when the kernels run;
+// Graph-capture variant of batched_flash_attention: the same schema, but the
+// row lengths come from cuda_offsets when the kernels run (prefill shapes are
+// planned on the device from them);
 // the CPU offsets are checked for shape only, so a graph captured once stays
 // valid while the caller rewrites cuda_offsets (and the caches) in place
 // between replays.  Output and workspace shapes depend on the tensor shapes
