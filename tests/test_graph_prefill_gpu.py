@@ -18,8 +18,8 @@ oracle's gates, and agree with the default operator (host-planned, other
 splits) within the same gates.  Shapes: Qwen3 chunks (G = 2, two query tiles
 per row, split rows merged), Qwen3.5 chunks (D = 256, G = 4), eight ragged
 Qwen3.5 rows (split and unsplit rows in one launch, cuts inside rows), head
-dim 64 with G = 1 (one tile), and a capacity that needs no split (no merge
-launch).
+dim 64 with G = 1 (one tile), 64 ragged rows with empty and one-query rows,
+and a capacity that needs no split (no merge launch).
 """
 
 import pytest
@@ -47,6 +47,11 @@ SHAPES = {
     "d64_group1": (8, 8, 64, 40, 1024, [
         [(40, 1024), (5, 500), (40, 40), (1, 1)],
         [(0, 9), (40, 900), (39, 1000), (12, 12)],
+    ]),
+    # 64 rows: a plan wave lane per row, a whole wave per priced split size.
+    "rows64": (16, 8, 64, 16, 2048, [
+        [(0 if r % 11 == 4 else (1 if r % 7 == 2 else 16 - r % 5), (r * 2654435761) % 2000 + 16) for r in range(64)],
+        [(16 if r % 3 else 5, 2048 if r % 9 == 0 else (r * 40503) % 600 + 16) for r in range(64)],
     ]),
     "no_split": (8, 4, 128, 16, 512, [
         [(16, 512), (1, 1), (16, 16), (0, 2)],
