@@ -36,7 +36,7 @@ enum {
   XINFER_ERR_SCALE = 7,           /* "Attention scale must be finite and positive" attention.cpp:103 */
   XINFER_ERR_OFFSETS_START = 8,   /* "Cumulative lengths must start at zero"       attention.cpp:35 */
   XINFER_ERR_LENGTHS = 9,         /* "Invalid query/KV lengths"                    attention.cpp:43-45 */
-  XINFER_ERR_WORKSPACE = 10,      /* workspace smaller than the *_workspace_size query */
+  XINFER_ERR_WORKSPACE = 10,      /* workspace smaller than its *_workspace_size, or not 16-byte aligned */
   XINFER_ERR_LAYOUT = 11,         /* feature stride != 1 or rows not 16-byte aligned */
   XINFER_ERR_CACHE = 12,          /* cache tensors not contiguous [B,H,C,D] / shape mismatch */
   XINFER_ERR_LAUNCH = 13,         /* a HIP kernel launch failed */

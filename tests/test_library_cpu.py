@@ -194,6 +194,12 @@ def test_workspace_size_is_a_pure_host_query(lib):
     host = (ctypes.c_int32 * len(offsets))(*offsets)
     bytes_ = lib.xinfer_batched_flash_attention_workspace_size(ctypes.byref(q), ctypes.byref(k), host)
     assert bytes_ > 0
+    # A workspace of that size that is not 16-byte aligned is refused before any launch.
+    assert lib.xinfer_batched_flash_attention(ctypes.byref(q), ctypes.byref(k), ctypes.byref(k), host, None,
+                                              ctypes.c_int64(0), ctypes.c_double(0.1), ctypes.c_void_p(1 << 20),
+                                              ctypes.c_void_p((1 << 22) + 8), ctypes.c_size_t(bytes_), None) == 10
+    assert lib.xinfer_status_string(10).decode() == (
+        "Attention workspace is smaller than its size query or not 16-byte aligned")
     # One short row with one split needs no partial records.
     q1, k1 = view([1, 16, 1, 128]), view([1, 8, 4096, 128])
     assert lib.xinfer_flash_attention_workspace_size(ctypes.byref(q1), ctypes.byref(k1), ctypes.c_int64(100)) == 0
@@ -276,6 +282,12 @@ def test_graph_mode_shapes_and_workspace(lib):
     assert graph(view([1, 16, 5, 128]), view([1, 8, 256, 128])) == 10   # prefill shapes: no workspace given
     assert graph(view([65, 16, 1, 128]), view([65, 8, 256, 128])) == 18
     assert graph(view([1, 16, 1, 128]), view([1, 8, 256, 128])) == 10   # no workspace given
+    qv, kv = view([2, 16, 64, 128]), view([2, 8, 1024, 128])
+    size = lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(qv), ctypes.byref(kv))
+    misaligned = lib.xinfer_batched_flash_attention_graph(
+        ctypes.byref(qv), ctypes.byref(kv), ctypes.byref(kv), ctypes.c_void_p(1 << 21), None, ctypes.c_int64(0),
+        ctypes.c_double(0.1), ctypes.c_void_p(1 << 20), ctypes.c_void_p((1 << 22) + 4), ctypes.c_size_t(size), None)
+    assert misaligned == 10
     assert lib.xinfer_batched_flash_attention_graph_workspace_size(ctypes.byref(view([1, 16, 1, 128])),
                                                                    ctypes.byref(view([1, 8, 128, 128]))) == 0
 

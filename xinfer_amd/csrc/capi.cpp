@@ -721,6 +721,15 @@ int check_capture(const xinfer_view4 *q, const xinfer_view4 *k, const xinfer_vie
   return XINFER_OK;
 }
 
+// The caller's workspace: at least `need` bytes, 16-byte aligned (the records
+// take 16-byte stores; the argument blocks planned on the device are read
+// with scalar loads).  A workspace of zero bytes may be null.
+int check_workspace(const void *workspace, size_t bytes, size_t need) {
+  if (bytes < need || (need && workspace == nullptr) || (reinterpret_cast<uintptr_t>(workspace) & 15u) != 0)
+    return XINFER_ERR_WORKSPACE;
+  return XINFER_OK;
+}
+
 int check_common(const xinfer_view4 &q, const xinfer_view4 &k, const xinfer_view4 &v, double scale) {
   if (!(std::isfinite(scale) && scale > 0)) return XINFER_ERR_SCALE;
   if (!attention_layout_ok(q) || !query_layout_ok(q) || !attention_layout_ok(k) ||
@@ -749,7 +758,7 @@ const char *xinfer_status_string(int status) {
     case XINFER_ERR_SCALE: return "Attention scale must be finite and positive";
     case XINFER_ERR_OFFSETS_START: return "Cumulative lengths must start at zero";
     case XINFER_ERR_LENGTHS: return "Invalid query/KV lengths";
-    case XINFER_ERR_WORKSPACE: return "Attention workspace is smaller than its size query";
+    case XINFER_ERR_WORKSPACE: return "Attention workspace is smaller than its size query or not 16-byte aligned";
     case XINFER_ERR_LAYOUT:
       return "Attention tensors need a unit feature stride, strides divisible by 8 and 16-byte "
              "aligned data";
@@ -789,8 +798,7 @@ int xinfer_batched_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k,
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
   const Plan plan = cached_plan(g, counts, lengths);
-  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
-    return XINFER_ERR_WORKSPACE;
+  if (int rc = check_workspace(workspace, workspace_bytes, plan.bytes())) return rc;
   return run_plan(plan, g, *q, *k, *v, blocks, blocks_stride, scale, contiguous_output(g, out), workspace,
                   static_cast<hipStream_t>(stream));
 }
@@ -813,7 +821,7 @@ int xinfer_batched_flash_attention_graph(const xinfer_view4 *q, const xinfer_vie
   if (int rc = check_blocks(blocks, blocks_stride)) return rc;
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (out == nullptr || device_offsets == nullptr) return XINFER_ERR_ARGUMENT;
-  if (workspace_bytes < cp.bytes() || (cp.bytes() && workspace == nullptr)) return XINFER_ERR_WORKSPACE;
+  if (int rc = check_workspace(workspace, workspace_bytes, cp.bytes())) return rc;
   CaptureArgs c{};
   c.q = view_of(*q);
   c.k = view_of(*k);
@@ -900,8 +908,7 @@ int xinfer_batched_flash_attention_out(const xinfer_view4 *q, const xinfer_view4
   if (g.B == 0 || g.T == 0) return XINFER_OK;
   if (int rc = check_output(g, out)) return rc;
   const Plan plan = cached_plan(g, counts, lengths);
-  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
-    return XINFER_ERR_WORKSPACE;
+  if (int rc = check_workspace(workspace, workspace_bytes, plan.bytes())) return rc;
   return run_plan(plan, g, *q, *k, *v, blocks, blocks_stride, scale, *out, workspace,
                   static_cast<hipStream_t>(stream));
 }
@@ -923,8 +930,7 @@ int xinfer_flash_attention(const xinfer_view4 *q, const xinfer_view4 *k, const x
   if (out == nullptr) return XINFER_ERR_ARGUMENT;
   std::vector<int32_t> counts(g.B, (int32_t)g.T), lengths(g.B, (int32_t)valid_length);
   const Plan plan = cached_plan(g, counts, lengths);
-  if (workspace_bytes < plan.bytes() || (plan.bytes() && workspace == nullptr))
-    return XINFER_ERR_WORKSPACE;
+  if (int rc = check_workspace(workspace, workspace_bytes, plan.bytes())) return rc;
   return run_plan(plan, g, *q, *k, *v, nullptr, 0, scale, contiguous_output(g, out), workspace,
                   static_cast<hipStream_t>(stream));
 }
