@@ -64,3 +64,22 @@ SHAPES = {
 @torch.inference_mode()
 def test_one_captured_prefill_step_replays_every_length_set(gpu_ops, name):
     replay_length_sets(gpu_ops, name, SHAPES[name])
+
+
+@torch.inference_mode()
+def test_device_counts_beyond_the_capacity_are_clamped(gpu_ops):
+    """Device lengths are not validated on the host: a count above the cache
+    capacity (here T = 40 queries over C = 32 slots) is taken as min(T, C)
+    queries over C keys, and the queries past it are zeroed -- a wrong row,
+    never an access outside the tensors."""
+    from test_graph_decode_gpu import check_oracle, metadata
+
+    heads, kv_heads, dim, tokens, capacity = 8, 4, 64, 40, 32
+    generator = torch.Generator().manual_seed(40)
+    q = torch.randn(2, heads, tokens, dim, generator=generator).to(torch.bfloat16).cuda()
+    k = torch.randn(2, kv_heads, capacity, dim, generator=generator).to(torch.bfloat16).cuda()
+    v = torch.randn(2, kv_heads, capacity, dim, generator=generator).to(torch.bfloat16).cuda()
+    host, cu, blocks = metadata([(40, 40), (5, 20)])
+    out = gpu_ops.batched_flash_attention_graph(q, k, v, host, cu, blocks, dim**-0.5)
+    torch.cuda.synchronize()
+    check_oracle(out, q, k, v, [(32, 32), (5, 20)], dim**-0.5)
